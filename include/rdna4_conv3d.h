@@ -1,0 +1,134 @@
+/*
+ * rdna4_conv3d.h -- C ABI of the gfx950 (MI355X) Conv3d / ConvTranspose3d library.
+ *
+ * The library (librdna4_conv3d_hip.so) implements the hot path of the
+ * reference package's autograd Functions as hand-written HIP kernels on CDNA4
+ * bf16/fp16 MFMA (v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulate):
+ *
+ *   Conv3d k=1 / k=3, stride 1, dilation 1, groups 1: forward, dX, dW (+ fused db)
+ *   ConvTranspose3d k=2, stride 2, pad 0:            forward, dX, dW (+ fused db)
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers on the current HIP device.  The caller
+ *     owns every buffer (inputs, outputs and the workspace); nothing is
+ *     allocated inside the library.
+ *   - Activations are 5-D [n, c, d, h, w] with arbitrary element strides given
+ *     in the descriptor, so NCDHW (contiguous) and NDHWC (channels_last_3d) are
+ *     both read and written natively, without layout copies.
+ *   - Weights are contiguous in PyTorch's parameter layout: Conv3d
+ *     (Cout, Cin, k, k, k); ConvTranspose3d (Cin, Cout, 2, 2, 2).
+ *   - `stream` is a hipStream_t (0 = the null stream).  Work is enqueued
+ *     asynchronously; nothing synchronises.
+ *   - Return value: R3C_OK (0), R3C_UNSUPPORTED (1: the caller should run its
+ *     own fallback, e.g. F.conv3d), R3C_INVALID (2: bad argument) or
+ *     R3C_HIP_ERROR (3: a HIP launch failed).  On any non-zero return,
+ *     r3c_last_error() describes the problem (thread-local string).
+ *   - Calls are re-entrant; the only global state is a thread-safe cache of
+ *     per-device properties.
+ *
+ * Which reference interface each entry replaces is cited per function
+ * (paths relative to the reference repository root).
+ */
+#ifndef RDNA4_CONV3D_H
+#define RDNA4_CONV3D_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define R3C_ABI_VERSION 1
+
+enum r3c_status {
+  R3C_OK = 0,
+  R3C_UNSUPPORTED = 1,
+  R3C_INVALID = 2,
+  R3C_HIP_ERROR = 3
+};
+
+enum r3c_dtype {
+  R3C_F16 = 0,
+  R3C_BF16 = 1,
+  R3C_F32 = 2
+};
+
+/* Geometry of one convolution, described in forward terms.
+ *   x: [n, cin, d, h, w]      y: [n, cout, od, oh, ow]
+ * Conv3d:          kernel 1 or 3, od = d + 2*pad_d - kernel + 1 (likewise h, w).
+ * ConvTranspose3d: kernel 2 (stride 2, pad 0), od = 2*d (likewise h, w).
+ * For the backward entry points x_strides describe dX (or x) and y_strides
+ * describe dY, i.e. the same tensors' roles as in forward. */
+typedef struct r3c_conv_desc {
+  int32_t dtype;                 /* R3C_F16 or R3C_BF16: x, w, bias, y, dy, dx */
+  int32_t n, cin, d, h, w;
+  int32_t cout, od, oh, ow;
+  int32_t kernel;                /* 1, 3 (Conv3d) or 2 (ConvTranspose3d k2s2) */
+  int32_t pad_d, pad_h, pad_w;   /* Conv3d zero padding; 0 for ConvTranspose3d */
+  int64_t x_strides[5];          /* element strides of x / dX, order (n, c, d, h, w) */
+  int64_t y_strides[5];          /* element strides of y / dY, order (n, c, d, h, w) */
+} r3c_conv_desc;
+
+/* Library identity.  No reference counterpart (the reference's native module
+ * is JIT-built by hip_backend.py:10-25 and has no version query). */
+int32_t r3c_abi_version(void);
+const char* r3c_last_error(void);
+/* 1 when `device` is a gfx950 GPU the kernels were built for, else 0.
+ * Replaces the arch gate _is_rdna4() (src/rdna4_conv3d/conv3d_wmma.py:44-48). */
+int32_t r3c_device_supported(int32_t device);
+
+/* ---- Conv3d forward: y = conv3d(x, w) + bias ------------------------------
+ * Replaces _launch_fwd -> _fwd_k3_kernel / _fwd_k1_kernel / _fwd_kernel
+ * (src/rdna4_conv3d/conv3d_wmma.py:1048-1105, 328-444) and the HIP fprop
+ * fwd_k3 (src/rdna4_conv3d/conv3d_wmma_hip.hip:148-195).
+ * bias may be NULL.  Workspace holds the MFMA-packed weight. */
+int64_t r3c_conv3d_fwd_workspace(const r3c_conv_desc* desc);
+int32_t r3c_conv3d_fwd(const r3c_conv_desc* desc, const void* x, const void* w,
+                       const void* bias, void* y, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* ---- Conv3d dX = conv3d_input(dy, w) ---------------------------------------
+ * Replaces _launch_dgrad (src/rdna4_conv3d/conv3d_wmma.py:1108-1179): k3 dX is
+ * the forward kernel over dy with the flipped, transposed weight and padding
+ * kernel-1-pad (the reference reuses `pad`, correct only for pad=1). */
+int64_t r3c_conv3d_dx_workspace(const r3c_conv_desc* desc);
+int32_t r3c_conv3d_dx(const r3c_conv_desc* desc, const void* dy, const void* w,
+                      void* dx, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/* ---- Conv3d dW = conv3d_weight(x, dy) and db = sum(dy) ---------------------
+ * Replaces _launch_wgrad -> _wgrad_kernel + partial.sum(0)
+ * (src/rdna4_conv3d/conv3d_wmma.py:1182-1214, 544-634) and the bias gradient
+ * go.sum(dim=(0,2,3,4)) (conv3d_wmma.py:1318).  Deterministic: fixed split of
+ * the position range, fp32 partials, fixed-order reduction, no float atomics.
+ * dw is (Cout, Cin, k, k, k) contiguous of dw_dtype (R3C_F32 or desc->dtype);
+ * db (may be NULL) is [Cout] of db_dtype. */
+int64_t r3c_conv3d_dw_workspace(const r3c_conv_desc* desc);
+int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
+                      void* dw, int32_t dw_dtype, void* db, int32_t db_dtype,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- ConvTranspose3d k=2 s=2 ------------------------------------------------
+ * Replace transpose_k2s2_fwd / _dx / _dw (src/rdna4_conv3d/conv3d_wmma.py:
+ * 1462-1542, kernels 793-1012) and db = go.sum (conv3d_wmma.py:1576).
+ * w is (Cin, Cout, 2, 2, 2) contiguous; dw has the same layout. */
+int64_t r3c_convt_k2s2_fwd_workspace(const r3c_conv_desc* desc);
+int32_t r3c_convt_k2s2_fwd(const r3c_conv_desc* desc, const void* x,
+                           const void* w, const void* bias, void* y,
+                           void* workspace, int64_t workspace_bytes,
+                           void* stream);
+int64_t r3c_convt_k2s2_dx_workspace(const r3c_conv_desc* desc);
+int32_t r3c_convt_k2s2_dx(const r3c_conv_desc* desc, const void* dy,
+                          const void* w, void* dx, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+int64_t r3c_convt_k2s2_dw_workspace(const r3c_conv_desc* desc);
+int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* desc, const void* x,
+                          const void* dy, void* dw, int32_t dw_dtype, void* db,
+                          int32_t db_dtype, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RDNA4_CONV3D_H */

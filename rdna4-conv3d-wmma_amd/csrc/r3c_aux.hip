@@ -1,0 +1,129 @@
+// r3c_aux.hip -- weight packing into MFMA fragment order, and the fixed-order
+// reduction of the weight-gradient split partials.
+#include "r3c_device.h"
+#include "r3c_kernels.h"
+
+namespace r3c {
+
+// Packed layout: [chunk][step][colblock][lane][8], lane = 16 * g + j.  Lane
+// (g, j) of step s holds k group kg = 4 s + g = (tap, 8-channel group cg) and
+// column colblock * 16 + j, i.e. exactly the B operand the row kernel feeds to
+// v_mfma_f32_16x16x32.  Out-of-range k or columns are zero.
+//
+// Weight index maps (w is PyTorch's parameter layout):
+//   K1/K3 forward   : Conv3d w (Cout, Cin, t)      -> w[col][ci][tap]
+//                     (_pack_weight, src/rdna4_conv3d/conv3d_wmma.py:1023-1026)
+//   K1/K3 dX (+16)  : source channel = Cout index, column = Cin index,
+//                     tap flipped: w[ci][col][taps-1-tap]
+//                     (flip(2,3,4).transpose(0,1), conv3d_wmma.py:1156-1157)
+//   T2DX            : ConvTranspose w (Cin, Cout, 8) -> w[col][ci][tap]
+//   T2FWD           : column = tap * Cout + co     -> w[ci][co][tap]
+//                     (_tr_pack_w, conv3d_wmma.py:1453-1455, columns (tap, co))
+__global__ void pack_weight_kernel(const PackArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.total) return;
+  const int e = (int)(idx & 7);
+  const int lane = (int)((idx >> 3) & 63);
+  int64_t rest = idx >> 9;
+  const int nb = (int)(rest % a.nbt_pad);
+  rest /= a.nbt_pad;
+  const int s = (int)(rest % a.nstep);
+  const int chunk = (int)(rest / a.nstep);
+  const int g = lane >> 4, j = lane & 15;
+  const int g8 = a.ck / 8;
+  const int kg = 4 * s + g;
+  uint16_t v = 0;
+  if (kg < a.taps * g8) {
+    const int tap = kg / g8, cg = kg % g8;
+    const int ci = chunk * a.ck + cg * 8 + e;
+    const int col = nb * 16 + j;
+    if (ci < a.cs && col < a.ncols) {
+      const int mode = a.mode & 15;
+      const bool dx = (a.mode & 16) != 0;
+      if (mode == MODE_K1 || mode == MODE_K3) {
+        if (!dx) v = a.w[((int64_t)col * a.w_cin + ci) * a.taps + tap];
+        else v = a.w[((int64_t)ci * a.w_cin + col) * a.taps + (a.taps - 1 - tap)];
+      } else if (mode == MODE_T2DX) {
+        v = a.w[((int64_t)col * a.w_cout + ci) * 8 + tap];
+      } else if (mode == MODE_T2FWD) {
+        const int t8 = col / a.w_cout, co = col - t8 * a.w_cout;
+        v = a.w[((int64_t)ci * a.w_cout + co) * 8 + t8];
+      }
+    }
+  }
+  a.out[idx] = v;
+}
+
+void launch_pack(int dtype, const PackArgs& a, hipStream_t stream) {
+  (void)dtype;  // a raw 16-bit copy: the element type does not matter
+  const int64_t blocks = (a.total + 255) / 256;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_elem(void* base, int64_t i, int dtype, float v) {
+  (void)sizeof(T);
+  if (dtype == DT_F32) reinterpret_cast<float*>(base)[i] = v;
+  else if (dtype == DT_BF16) reinterpret_cast<uint16_t*>(base)[i] = from_f32<bf16_tag>(v);
+  else reinterpret_cast<uint16_t*>(base)[i] = from_f32<f16_tag>(v);
+}
+
+// One block = 64 output elements x 4 split quarters.  Quarter q adds splits
+// [q*S/4, (q+1)*S/4) in increasing order; the four quarter sums are then added
+// in the order 0, 1, 2, 3.  The result is bitwise reproducible run to run.
+// Elements [0, Fc*taps*Gc) are dW (walked with G fastest, matching the partial
+// layout for coalesced reads); the tail holds db.
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const ReduceArgs a) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63;
+  const int q = threadIdx.x >> 6;
+  const int64_t nw = (int64_t)a.Fc * a.taps * a.Gc;
+  const int ndb = a.db_mode == 1 ? a.Fc : (a.db_mode == 2 ? a.Gc : 0);
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+  const int s0 = (int)(((int64_t)q * a.nsplit) / 4);
+  const int s1 = (int)(((int64_t)(q + 1) * a.nsplit) / 4);
+  float sum = 0.f;
+  if (e < nw) {
+    const int gch = (int)(e % a.Gc);
+    const int64_t r = e / a.Gc;
+    const int tap = (int)(r % a.taps);
+    const int f = (int)(r / a.taps);
+    const size_t stride = (size_t)a.Fpad * a.taps * a.Gpad;
+    const float* p = a.part + ((size_t)f * a.taps + tap) * a.Gpad + gch;
+    for (int s = s0; s < s1; ++s) sum += p[(size_t)s * stride];
+  } else if (e < nw + ndb) {
+    const int c = (int)(e - nw);
+    if (a.db_mode == 1) {
+      for (int s = s0; s < s1; ++s) sum += a.dbpart[(size_t)s * a.Fpad + c];
+    } else {
+      for (int s = s0; s < s1; ++s) {
+        float t = 0.f;
+        for (int tap = 0; tap < a.taps; ++tap) t += a.dbpart[((size_t)s * a.taps + tap) * a.Gpad + c];
+        sum += t;
+      }
+    }
+  }
+  red[q][lane] = sum;
+  __syncthreads();
+  if (q == 0) {
+    const float tot = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    if (e < nw) {
+      const int gch = (int)(e % a.Gc);
+      const int64_t r = e / a.Gc;
+      const int tap = (int)(r % a.taps);
+      const int f = (int)(r / a.taps);
+      store_elem<float>(a.dw, ((int64_t)f * a.Gc + gch) * a.taps + tap, a.dw_dtype, tot);
+    } else if (e < nw + ndb) {
+      store_elem<float>(a.db, e - nw, a.db_dtype, tot);
+    }
+  }
+}
+
+void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream) {
+  const int64_t nw = (int64_t)a.Fc * a.taps * a.Gc;
+  const int ndb = a.db_mode == 1 ? a.Fc : (a.db_mode == 2 ? a.Gc : 0);
+  const int64_t blocks = (nw + ndb + 63) / 64;
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+}
+
+}  // namespace r3c

@@ -1,0 +1,292 @@
+"""ctypes binding of librdna4_conv3d_hip.so (the gfx950 kernels behind the C ABI
+declared in include/rdna4_conv3d.h).
+
+This module is the marshaller that replaces the reference's Triton launch
+wrappers (src/rdna4_conv3d/conv3d_wmma.py:1048-1214, 1462-1542): it builds the
+plain-C descriptor from tensor shapes and strides, allocates outputs (in the
+input's memory format) and the workspace through PyTorch's caching allocator,
+and enqueues the kernels on the current PyTorch stream.  Nothing is computed in
+Python.  There is no fallback here: if the library cannot be loaded, every
+call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+from typing import Optional, Sequence, Tuple
+
+import torch  # imported first: the library reuses the HIP runtime torch loaded
+
+LIB_NAME = "librdna4_conv3d_hip.so"
+ABI_VERSION = 1
+
+R3C_OK, R3C_UNSUPPORTED, R3C_INVALID, R3C_HIP_ERROR = 0, 1, 2, 3
+R3C_F16, R3C_BF16, R3C_F32 = 0, 1, 2
+
+_DTYPE_CODE = {torch.float16: R3C_F16, torch.bfloat16: R3C_BF16, torch.float32: R3C_F32}
+
+
+class ConvDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("n", ctypes.c_int32), ("cin", ctypes.c_int32), ("d", ctypes.c_int32),
+        ("h", ctypes.c_int32), ("w", ctypes.c_int32),
+        ("cout", ctypes.c_int32), ("od", ctypes.c_int32), ("oh", ctypes.c_int32),
+        ("ow", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
+        ("pad_d", ctypes.c_int32), ("pad_h", ctypes.c_int32), ("pad_w", ctypes.c_int32),
+        ("x_strides", ctypes.c_int64 * 5),
+        ("y_strides", ctypes.c_int64 * 5),
+    ]
+
+
+class NativeError(RuntimeError):
+    """A native entry point returned R3C_INVALID or R3C_HIP_ERROR."""
+
+
+class NativeUnsupported(RuntimeError):
+    """A native entry point returned R3C_UNSUPPORTED (caller may fall back)."""
+
+
+_lib = None
+_lib_err: Optional[str] = None
+_lock = threading.Lock()
+
+
+def library_path() -> Path:
+    override = os.environ.get("RDNA4_CONV3D_LIB")
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / LIB_NAME
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    D = ctypes.POINTER(ConvDesc)
+    lib.r3c_abi_version.restype = I32
+    lib.r3c_abi_version.argtypes = []
+    lib.r3c_last_error.restype = ctypes.c_char_p
+    lib.r3c_last_error.argtypes = []
+    lib.r3c_device_supported.restype = I32
+    lib.r3c_device_supported.argtypes = [I32]
+    for name in ("conv3d_fwd", "conv3d_dx", "conv3d_dw", "convt_k2s2_fwd", "convt_k2s2_dx", "convt_k2s2_dw"):
+        f = getattr(lib, f"r3c_{name}_workspace")
+        f.restype = I64
+        f.argtypes = [D]
+    for name in ("conv3d_fwd", "convt_k2s2_fwd"):
+        f = getattr(lib, f"r3c_{name}")
+        f.restype = I32
+        f.argtypes = [D, P, P, P, P, P, I64, P]
+    for name in ("conv3d_dx", "convt_k2s2_dx"):
+        f = getattr(lib, f"r3c_{name}")
+        f.restype = I32
+        f.argtypes = [D, P, P, P, P, I64, P]
+    for name in ("conv3d_dw", "convt_k2s2_dw"):
+        f = getattr(lib, f"r3c_{name}")
+        f.restype = I32
+        f.argtypes = [D, P, P, P, I32, P, I32, P, I64, P]
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the native library; raise RuntimeError if absent."""
+    global _lib, _lib_err
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        try:
+            lib = ctypes.CDLL(str(path))
+            _bind(lib)
+            ver = lib.r3c_abi_version()
+            if ver != ABI_VERSION:
+                raise RuntimeError(f"ABI version {ver}, expected {ABI_VERSION}")
+        except (OSError, AttributeError, RuntimeError) as e:
+            _lib_err = f"cannot load {path}: {e}"
+            raise RuntimeError(
+                f"rdna4_conv3d native library unavailable ({_lib_err}); "
+                "build it with `python __graft_entry__.py build` or "
+                "`python rdna4-conv3d-wmma_amd/build_native.py`") from e
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except RuntimeError:
+        return False
+
+
+def device_supported(device_index: int) -> bool:
+    return bool(load().r3c_device_supported(int(device_index)))
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _dims5(t: torch.Tensor) -> Tuple[int, ...]:
+    if t.dim() != 5:
+        raise ValueError(f"expected a 5-D tensor, got {tuple(t.shape)}")
+    return tuple(int(s) for s in t.shape)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream_handle(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _check(lib, rc: int, what: str) -> None:
+    if rc == R3C_OK:
+        return
+    msg = lib.r3c_last_error().decode(errors="replace")
+    if rc == R3C_UNSUPPORTED:
+        raise NativeUnsupported(f"{what}: {msg}")
+    raise NativeError(f"{what} failed (code {rc}): {msg}")
+
+
+def is_channels_last(t: torch.Tensor) -> bool:
+    return t.dim() == 5 and t.is_contiguous(memory_format=torch.channels_last_3d)
+
+
+def _dense(t: torch.Tensor) -> torch.Tensor:
+    """NCDHW-contiguous or channels_last_3d tensors pass through; others are densified."""
+    if t.is_contiguous() or is_channels_last(t):
+        return t
+    return t.contiguous()
+
+
+def _empty_like_layout(shape: Sequence[int], like: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    fmt = torch.channels_last_3d if (is_channels_last(like) and not like.is_contiguous()) else torch.contiguous_format
+    return torch.empty(tuple(shape), device=like.device, dtype=dtype, memory_format=fmt)
+
+
+def make_desc(x_shape, y_shape, kernel: int, padding, dtype: torch.dtype, x_strides, y_strides) -> ConvDesc:
+    d = ConvDesc()
+    d.dtype = _DTYPE_CODE[dtype]
+    d.n, d.cin, d.d, d.h, d.w = (int(v) for v in x_shape)
+    _, d.cout, d.od, d.oh, d.ow = (int(v) for v in y_shape)
+    d.kernel = int(kernel)
+    d.pad_d, d.pad_h, d.pad_w = (int(p) for p in padding)
+    for i in range(5):
+        d.x_strides[i] = int(x_strides[i])
+        d.y_strides[i] = int(y_strides[i])
+    return d
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# Conv3d
+# ---------------------------------------------------------------------------
+def conv3d_fwd(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], padding,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = conv3d(x, weight) + bias; stride 1, k in {1, 3}.  y keeps x's layout."""
+    lib = load()
+    x = _dense(x)
+    weight = weight.contiguous()
+    n, cin, d, h, w = _dims5(x)
+    cout, k = int(weight.shape[0]), int(weight.shape[2])
+    od, oh, ow = (d + 2 * padding[0] - k + 1, h + 2 * padding[1] - k + 1, w + 2 * padding[2] - k + 1)
+    y = out if out is not None else _empty_like_layout((n, cout, od, oh, ow), x, x.dtype)
+    desc = make_desc(x.shape, y.shape, k, padding, x.dtype, x.stride(), y.stride())
+    ws = _workspace(lib.r3c_conv3d_fwd_workspace(ctypes.byref(desc)), x.device)
+    b = bias.contiguous() if bias is not None else None
+    rc = lib.r3c_conv3d_fwd(ctypes.byref(desc), _ptr(x), _ptr(weight), _ptr(b), _ptr(y), _ptr(ws),
+                            ws.numel(), _stream_handle(x.device))
+    _check(lib, rc, "r3c_conv3d_fwd")
+    return y
+
+
+def conv3d_dx(go: torch.Tensor, weight: torch.Tensor, x_shape, padding, like: torch.Tensor) -> torch.Tensor:
+    """dX of a stride-1 Conv3d; dX takes `like`'s memory format."""
+    lib = load()
+    go = _dense(go)
+    weight = weight.contiguous()
+    k = int(weight.shape[2])
+    gx = _empty_like_layout(tuple(int(v) for v in x_shape), like, go.dtype)
+    desc = make_desc(gx.shape, go.shape, k, padding, go.dtype, gx.stride(), go.stride())
+    ws = _workspace(lib.r3c_conv3d_dx_workspace(ctypes.byref(desc)), go.device)
+    rc = lib.r3c_conv3d_dx(ctypes.byref(desc), _ptr(go), _ptr(weight), _ptr(gx), _ptr(ws), ws.numel(),
+                           _stream_handle(go.device))
+    _check(lib, rc, "r3c_conv3d_dx")
+    return gx
+
+
+def conv3d_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, padding, dw_dtype: torch.dtype,
+              want_db: bool = False, db_dtype: Optional[torch.dtype] = None):
+    """(dW in OIDHW of dw_dtype, db or None).  Deterministic split-K."""
+    lib = load()
+    x = _dense(x)
+    go = _dense(go)
+    k = int(weight_shape[2])
+    desc = make_desc(x.shape, go.shape, k, padding, x.dtype, x.stride(), go.stride())
+    dw = torch.empty(tuple(int(v) for v in weight_shape), device=x.device, dtype=dw_dtype)
+    db = None
+    if want_db:
+        db = torch.empty((int(weight_shape[0]),), device=x.device, dtype=db_dtype or dw_dtype)
+    ws = _workspace(lib.r3c_conv3d_dw_workspace(ctypes.byref(desc)), x.device)
+    rc = lib.r3c_conv3d_dw(ctypes.byref(desc), _ptr(x), _ptr(go), _ptr(dw), _DTYPE_CODE[dw_dtype], _ptr(db),
+                           _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws), ws.numel(),
+                           _stream_handle(x.device))
+    _check(lib, rc, "r3c_conv3d_dw")
+    return dw, db
+
+
+# ---------------------------------------------------------------------------
+# ConvTranspose3d k=2 s=2
+# ---------------------------------------------------------------------------
+def convt_fwd(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    lib = load()
+    x = _dense(x)
+    weight = weight.contiguous()
+    n, cin, d, h, w = _dims5(x)
+    cout = int(weight.shape[1])
+    y = _empty_like_layout((n, cout, 2 * d, 2 * h, 2 * w), x, x.dtype)
+    desc = make_desc(x.shape, y.shape, 2, (0, 0, 0), x.dtype, x.stride(), y.stride())
+    ws = _workspace(lib.r3c_convt_k2s2_fwd_workspace(ctypes.byref(desc)), x.device)
+    b = bias.contiguous() if bias is not None else None
+    rc = lib.r3c_convt_k2s2_fwd(ctypes.byref(desc), _ptr(x), _ptr(weight), _ptr(b), _ptr(y), _ptr(ws),
+                                ws.numel(), _stream_handle(x.device))
+    _check(lib, rc, "r3c_convt_k2s2_fwd")
+    return y
+
+
+def convt_dx(go: torch.Tensor, weight: torch.Tensor, x_shape, like: torch.Tensor) -> torch.Tensor:
+    lib = load()
+    go = _dense(go)
+    weight = weight.contiguous()
+    gx = _empty_like_layout(tuple(int(v) for v in x_shape), like, go.dtype)
+    desc = make_desc(gx.shape, go.shape, 2, (0, 0, 0), go.dtype, gx.stride(), go.stride())
+    ws = _workspace(lib.r3c_convt_k2s2_dx_workspace(ctypes.byref(desc)), go.device)
+    rc = lib.r3c_convt_k2s2_dx(ctypes.byref(desc), _ptr(go), _ptr(weight), _ptr(gx), _ptr(ws), ws.numel(),
+                               _stream_handle(go.device))
+    _check(lib, rc, "r3c_convt_k2s2_dx")
+    return gx
+
+
+def convt_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, dw_dtype: torch.dtype, want_db: bool = False,
+             db_dtype: Optional[torch.dtype] = None):
+    lib = load()
+    x = _dense(x)
+    go = _dense(go)
+    desc = make_desc(x.shape, go.shape, 2, (0, 0, 0), x.dtype, x.stride(), go.stride())
+    dw = torch.empty(tuple(int(v) for v in weight_shape), device=x.device, dtype=dw_dtype)
+    db = None
+    if want_db:
+        db = torch.empty((int(weight_shape[1]),), device=x.device, dtype=db_dtype or dw_dtype)
+    ws = _workspace(lib.r3c_convt_k2s2_dw_workspace(ctypes.byref(desc)), x.device)
+    rc = lib.r3c_convt_k2s2_dw(ctypes.byref(desc), _ptr(x), _ptr(go), _ptr(dw), _DTYPE_CODE[dw_dtype], _ptr(db),
+                               _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws), ws.numel(),
+                               _stream_handle(x.device))
+    _check(lib, rc, "r3c_convt_k2s2_dw")
+    return dw, db

@@ -1,0 +1,145 @@
+"""GPU parity of the native HIP kernels against the fp32/fp64 reference path.
+
+Inputs are generated on the CPU with fixed seeds, rounded to bf16/fp16, and the
+reference is computed in float64 from the same rounded values (F.conv3d /
+conv_transpose3d / autograd on the CPU, the reference package's own oracle), and
+at the smallest shapes also by the C oracle.  Tolerances (north star):
+max|out - ref| / max|ref| <= 1e-2 for fwd and dX, <= 3e-2 for dW.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _util import gen, kaiming_weight, max_rel, to_layout
+
+pytestmark = pytest.mark.gpu
+
+TOL_FWD = 1e-2
+TOL_DX = 1e-2
+TOL_DW = 3e-2
+
+
+def _gpu_ok():
+    if not torch.cuda.is_available():
+        return False
+    return (torch.cuda.get_device_properties(0).gcnArchName or "").startswith("gfx950")
+
+
+requires_gfx950 = pytest.mark.skipif(not _gpu_ok(), reason="needs a gfx950 GPU")
+
+
+def _native():
+    from rdna4_conv3d import _native
+    _native.load()
+    return _native
+
+
+def _ref_conv(x, w, b, pad, go):
+    """float64 CPU reference: y, dx, dw, db from the same rounded inputs."""
+    xd = x.detach().double().cpu().requires_grad_(True)
+    wd = w.detach().double().cpu().requires_grad_(True)
+    bd = None if b is None else b.detach().double().cpu().requires_grad_(True)
+    y = F.conv3d(xd, wd, bd, 1, pad)
+    y.backward(go.detach().double().cpu())
+    return y.detach(), xd.grad, wd.grad, (None if bd is None else bd.grad)
+
+
+CONV_CASES = [
+    # (n, cin, cout, d, h, w, k, pad)  -- the reference's test_conv3d.py:51-54 shapes first
+    (2, 5, 7, 9, 11, 13, 3, 1),
+    (2, 24, 1, 8, 16, 16, 1, 0),
+    (1, 24, 24, 8, 16, 16, 3, 1),
+    (1, 1, 24, 8, 16, 16, 3, 1),
+    (1, 8, 16, 6, 7, 9, 3, 0),
+    (1, 8, 16, 6, 7, 9, 3, 2),
+    (1, 16, 8, 5, 6, 7, 1, 1),
+    (1, 48, 48, 8, 8, 16, 3, 1),
+    (1, 40, 96, 4, 8, 16, 3, 1),
+    (1, 96, 40, 4, 8, 20, 3, 1),
+    (2, 48, 24, 4, 9, 33, 1, 0),
+]
+
+
+@requires_gfx950
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "n{}c{}-{}_{}x{}x{}_k{}p{}".format(*c))
+def test_conv3d_native_parity(case, layout, dtype):
+    nat = _native()
+    n, cin, cout, d, h, w, k, pad = case
+    print(f"case conv {case} {layout} {dtype}", flush=True)
+    x = gen((n, cin, d, h, w), 0, dtype)
+    wt = kaiming_weight((cout, cin, k, k, k), cin * k ** 3, 1, dtype)
+    b = gen((cout,), 4, dtype)
+    od, oh, ow = d + 2 * pad - k + 1, h + 2 * pad - k + 1, w + 2 * pad - k + 1
+    go = gen((n, cout, od, oh, ow), 2, dtype)
+    y_ref, dx_ref, dw_ref, db_ref = _ref_conv(x, wt, b, pad, go)
+
+    xg = to_layout(x.cuda(), layout)
+    gog = to_layout(go.cuda(), layout)
+    wg, bg = wt.cuda(), b.cuda()
+    y = nat.conv3d_fwd(xg, wg, bg, (pad, pad, pad))
+    dx = nat.conv3d_dx(gog, wg, xg.shape, (pad, pad, pad), like=xg)
+    dw, db = nat.conv3d_dw(xg, gog, wg.shape, (pad, pad, pad), torch.float32, want_db=True, db_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert y.shape == y_ref.shape and dx.shape == dx_ref.shape and dw.shape == dw_ref.shape
+    if layout == "ndhwc" and not xg.is_contiguous():
+        # outputs follow the input layout; a tensor that is both NCDHW- and
+        # NDHWC-contiguous (C == 1) counts as NCDHW, as in torch
+        assert y.is_contiguous(memory_format=torch.channels_last_3d)
+        assert dx.is_contiguous(memory_format=torch.channels_last_3d)
+    e_y, e_dx, e_dw, e_db = max_rel(y, y_ref), max_rel(dx, dx_ref), max_rel(dw, dw_ref), max_rel(db, db_ref)
+    print(f"  maxrel y {e_y:.2e} dx {e_dx:.2e} dw {e_dw:.2e} db {e_db:.2e}", flush=True)
+    assert e_y <= TOL_FWD
+    assert e_dx <= TOL_DX
+    assert e_dw <= TOL_DW
+    assert e_db <= TOL_DW
+
+
+CONVT_CASES = [
+    # (n, cin, cout, d, h, w)
+    (1, 16, 8, 3, 4, 5),
+    (2, 24, 48, 2, 3, 17),
+    (1, 48, 24, 4, 8, 16),
+    (1, 192, 96, 2, 4, 16),
+    (1, 5, 3, 2, 2, 3),
+]
+
+
+def _ref_convt(x, w, b, go):
+    xd = x.detach().double().cpu().requires_grad_(True)
+    wd = w.detach().double().cpu().requires_grad_(True)
+    bd = None if b is None else b.detach().double().cpu().requires_grad_(True)
+    y = F.conv_transpose3d(xd, wd, bd, stride=2)
+    y.backward(go.detach().double().cpu())
+    return y.detach(), xd.grad, wd.grad, (None if bd is None else bd.grad)
+
+
+@requires_gfx950
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("case", CONVT_CASES, ids=lambda c: "n{}c{}-{}_{}x{}x{}".format(*c))
+def test_convt_native_parity(case, layout, dtype):
+    nat = _native()
+    n, cin, cout, d, h, w = case
+    print(f"case convt {case} {layout} {dtype}", flush=True)
+    x = gen((n, cin, d, h, w), 0, dtype)
+    wt = kaiming_weight((cin, cout, 2, 2, 2), cout * 8, 1, dtype)
+    b = gen((cout,), 4, dtype)
+    go = gen((n, cout, 2 * d, 2 * h, 2 * w), 2, dtype)
+    y_ref, dx_ref, dw_ref, db_ref = _ref_convt(x, wt, b, go)
+    xg = to_layout(x.cuda(), layout)
+    gog = to_layout(go.cuda(), layout)
+    wg, bg = wt.cuda(), b.cuda()
+    y = nat.convt_fwd(xg, wg, bg)
+    dx = nat.convt_dx(gog, wg, xg.shape, like=xg)
+    dw, db = nat.convt_dw(xg, gog, wg.shape, torch.float32, want_db=True, db_dtype=torch.float32)
+    torch.cuda.synchronize()
+    e_y, e_dx, e_dw, e_db = max_rel(y, y_ref), max_rel(dx, dx_ref), max_rel(dw, dw_ref), max_rel(db, db_ref)
+    print(f"  maxrel y {e_y:.2e} dx {e_dx:.2e} dw {e_dw:.2e} db {e_db:.2e}", flush=True)
+    assert e_y <= TOL_FWD
+    assert e_dx <= TOL_DX
+    assert e_dw <= TOL_DW
+    assert e_db <= TOL_DW
