@@ -127,6 +127,19 @@ int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* desc, const void* x,
                           int32_t db_dtype, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* ---- Kernel timing hook (measurement only) ----------------------------------
+ * No counterpart in the reference (its benches time whole calls with
+ * time.perf_counter, benches/isolated.py:26-34).  While enabled, each kernel
+ * launch is bracketed by HIP events on its own launch stream and tagged with
+ * the calling thread's current tag and a kernel family
+ * (0 weight pack, 1 row kernel, 2 weight-gradient kernel, 3 split reduce).
+ * r3c_timing_collect waits for the recorded events, writes up to max_records
+ * (tag, kind, milliseconds) triples, clears the records and returns how many
+ * launches were recorded. */
+int32_t r3c_timing_enable(int32_t on);
+void r3c_timing_set_tag(int32_t tag);
+int32_t r3c_timing_collect(int32_t max_records, int32_t* tags, int32_t* kinds, float* ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "r3c_kernels.h"
 #include "rdna4_conv3d.h"
@@ -62,6 +63,65 @@ int ok() {
   g_err.clear();
   return R3C_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Kernel timing hook (measurement only).  While enabled, each kernel launch is
+// bracketed by a pair of HIP events on its own launch stream, tagged with the
+// caller's current tag and the kernel family; collect() waits for them and
+// returns the per-launch durations.
+// ---------------------------------------------------------------------------
+enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3 };
+
+struct TimingRec {
+  int tag, kind;
+  hipEvent_t e0, e1;
+};
+
+struct TimingState {
+  std::mutex mu;
+  bool on = false;
+  std::vector<TimingRec> recs;
+  std::vector<hipEvent_t> pool;
+};
+
+TimingState& timing() {
+  static TimingState* st = new TimingState();  // lives for the process
+  return *st;
+}
+
+thread_local int g_tag = 0;
+
+hipEvent_t pool_event(TimingState& st) {
+  if (!st.pool.empty()) {
+    hipEvent_t e = st.pool.back();
+    st.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+struct TimedLaunch {
+  TimingState& st;
+  hipStream_t s;
+  int kind;
+  hipEvent_t e0 = nullptr;
+  bool active = false;
+  TimedLaunch(int k, hipStream_t stream) : st(timing()), s(stream), kind(k) {
+    std::lock_guard<std::mutex> lk(st.mu);
+    if (!st.on) return;
+    e0 = pool_event(st);
+    if (e0 && hipEventRecord(e0, s) == hipSuccess) active = true;
+  }
+  void end() {
+    if (!active) return;
+    std::lock_guard<std::mutex> lk(st.mu);
+    hipEvent_t e1 = pool_event(st);
+    if (e1 && hipEventRecord(e1, s) == hipSuccess) st.recs.push_back({g_tag, kind, e0, e1});
+    active = false;
+  }
+};
 
 constexpr int64_t kMaxLds = 160 * 1024;
 constexpr int kWgTarget = 512;                 // weight-gradient workgroups to aim for
@@ -289,7 +349,11 @@ int run_fwd(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   PackArgs pk = p.pk;
   pk.w = static_cast<const uint16_t*>(w);
   pk.out = static_cast<uint16_t*>(ws);
-  launch_pack(d->dtype, pk, s);
+  {
+    TimedLaunch tl(KIND_PACK, s);
+    launch_pack(d->dtype, pk, s);
+    tl.end();
+  }
   rc = check_launch("weight pack");
   if (rc) return rc;
   FwdArgs a = p.a;
@@ -301,7 +365,10 @@ int run_fwd(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   const int64_t blocks = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
   if (blocks >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
   a.nblocks = (int32_t)blocks;
-  if (!launch_igemm_fwd(d->dtype, p.mode, p.ck, p.nb, a, p.lds, s))
+  TimedLaunch tl(KIND_ROW, s);
+  const bool launched = launch_igemm_fwd(d->dtype, p.mode, p.ck, p.nb, a, p.lds, s);
+  tl.end();
+  if (!launched)
     return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d", p.mode, p.ck, p.nb);
   return check_launch("row kernel");
 }
@@ -451,7 +518,10 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   a.f_cl = vec16_ok(a.fsrc, a.fs) ? 1 : 0;
   a.g_cl = vec16_ok(a.gsrc, a.gs) ? 1 : 0;
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
-  if (!launch_igemm_wgrad(d->dtype, p.mode, p.fb, p.cbw, a, p.lds, s))
+  TimedLaunch tl(KIND_WGRAD, s);
+  const bool launched = launch_igemm_wgrad(d->dtype, p.mode, p.fb, p.cbw, a, p.lds, s);
+  tl.end();
+  if (!launched)
     return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d fb %d cbw %d", p.mode, p.fb, p.cbw);
   rc = check_launch("weight-gradient kernel");
   if (rc) return rc;
@@ -470,7 +540,11 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   r.dw_dtype = dw_dtype;
   r.db_dtype = db_dtype;
   r.db_mode = a.db_mode;
-  launch_wgrad_reduce(r, s);
+  {
+    TimedLaunch tr(KIND_REDUCE, s);
+    launch_wgrad_reduce(r, s);
+    tr.end();
+  }
   return check_launch("weight-gradient reduce");
 }
 
@@ -560,6 +634,35 @@ int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* d, const void* x, const void* dy,
   int rc = validate(d, true);
   if (rc) return rc;
   return run_wgrad(d, true, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
+}
+
+int32_t r3c_timing_enable(int32_t on) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  st.on = on != 0;
+  return R3C_OK;
+}
+
+void r3c_timing_set_tag(int32_t tag) { g_tag = tag; }
+
+int32_t r3c_timing_collect(int32_t max_records, int32_t* tags, int32_t* kinds, float* ms) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  int32_t n = 0;
+  for (const TimingRec& r : st.recs) {
+    float t = -1.f;
+    if (hipEventSynchronize(r.e1) == hipSuccess && hipEventElapsedTime(&t, r.e0, r.e1) != hipSuccess) t = -1.f;
+    if (n < max_records) {
+      if (tags) tags[n] = r.tag;
+      if (kinds) kinds[n] = r.kind;
+      if (ms) ms[n] = t;
+    }
+    ++n;
+    st.pool.push_back(r.e0);
+    st.pool.push_back(r.e1);
+  }
+  st.recs.clear();
+  return n;
 }
 
 }  // extern "C"

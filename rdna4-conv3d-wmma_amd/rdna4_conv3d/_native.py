@@ -87,6 +87,12 @@ def _bind(lib: ctypes.CDLL) -> None:
         f = getattr(lib, f"r3c_{name}")
         f.restype = I32
         f.argtypes = [D, P, P, P, I32, P, I32, P, I64, P]
+    lib.r3c_timing_enable.restype = I32
+    lib.r3c_timing_enable.argtypes = [I32]
+    lib.r3c_timing_set_tag.restype = None
+    lib.r3c_timing_set_tag.argtypes = [I32]
+    lib.r3c_timing_collect.restype = I32
+    lib.r3c_timing_collect.argtypes = [I32, ctypes.POINTER(I32), ctypes.POINTER(I32), ctypes.POINTER(ctypes.c_float)]
 
 
 def load() -> ctypes.CDLL:
@@ -124,6 +130,29 @@ def available() -> bool:
 
 def device_supported(device_index: int) -> bool:
     return bool(load().r3c_device_supported(int(device_index)))
+
+
+KERNEL_KINDS = ("pack", "row", "wgrad", "reduce")
+
+
+def timing_enable(on: bool) -> None:
+    """Start (clearing old records) or stop per-launch kernel timing in the library."""
+    load().r3c_timing_enable(1 if on else 0)
+
+
+def timing_tag(tag: int) -> None:
+    """Tag attached to the kernels this thread launches next."""
+    load().r3c_timing_set_tag(int(tag))
+
+
+def timing_collect(max_records: int = 1 << 16):
+    """Wait for recorded launches; return [(tag, kind name, ms)] and clear them."""
+    lib = load()
+    tags = (ctypes.c_int32 * max_records)()
+    kinds = (ctypes.c_int32 * max_records)()
+    ms = (ctypes.c_float * max_records)()
+    n = lib.r3c_timing_collect(max_records, tags, kinds, ms)
+    return [(int(tags[i]), KERNEL_KINDS[kinds[i]], float(ms[i])) for i in range(min(n, max_records))]
 
 
 # ---------------------------------------------------------------------------
