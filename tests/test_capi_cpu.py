@@ -1,0 +1,100 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, agrees with the header on the ABI version and the descriptor
+layout, and validates descriptors on the host (no compute calls here)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from rdna4_conv3d import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "rdna4_conv3d.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(r3c_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    names = _declared()
+    assert len(names) >= 18
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.library_path())], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (r3c_\w+)", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for n in names:
+        assert getattr(lib, n) is not None
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define R3C_ABI_VERSION (\d+)", HEADER.read_text())
+    assert _native.load().r3c_abi_version() == int(m.group(1)) == _native.ABI_VERSION
+
+
+def test_descriptor_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "rdna4_conv3d.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu\\n\", sizeof(r3c_conv_desc), offsetof(r3c_conv_desc, kernel),"
+        " offsetof(r3c_conv_desc, x_strides), offsetof(r3c_conv_desc, y_strides)); return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    D = _native.ConvDesc
+    assert [int(v) for v in got] == [ctypes.sizeof(D), D.kernel.offset, D.x_strides.offset, D.y_strides.offset]
+
+
+def _desc(k=3, pad=1, n=2, cin=8, cout=16, sp=(6, 7, 9), transpose=False, dtype=_native.R3C_BF16):
+    import torch
+    d, h, w = sp
+    if transpose:
+        od, oh, ow = 2 * d, 2 * h, 2 * w
+    else:
+        od, oh, ow = d + 2 * pad - k + 1, h + 2 * pad - k + 1, w + 2 * pad - k + 1
+    x = torch.empty(n, cin, d, h, w)
+    y = torch.empty(n, cout, od, oh, ow)
+    desc = _native.make_desc(x.shape, y.shape, k, (pad,) * 3, torch.bfloat16, x.stride(), y.stride())
+    desc.dtype = dtype
+    return desc
+
+
+def test_workspace_queries_validate_on_host():
+    lib = _native.load()
+    ok = _desc()
+    assert lib.r3c_conv3d_fwd_workspace(ctypes.byref(ok)) > 0
+    assert lib.r3c_conv3d_dx_workspace(ctypes.byref(ok)) > 0
+    assert lib.r3c_conv3d_dw_workspace(ctypes.byref(ok)) > 0
+    t = _desc(k=2, pad=0, transpose=True)
+    for name in ("fwd", "dx", "dw"):
+        assert getattr(lib, f"r3c_convt_k2s2_{name}_workspace")(ctypes.byref(t)) > 0
+    assert lib.r3c_conv3d_fwd_workspace(ctypes.byref(_desc(k=5, pad=2))) == -1   # kernel 5
+    bad = _desc()
+    bad.od += 1                                                                  # inconsistent dims
+    assert lib.r3c_conv3d_fwd_workspace(ctypes.byref(bad)) == -1
+    assert lib.r3c_conv3d_fwd_workspace(ctypes.byref(_desc(dtype=_native.R3C_F32))) == -1
+    assert lib.r3c_convt_k2s2_fwd_workspace(ctypes.byref(ok)) == -1             # k3 desc on ConvT
+
+
+def test_invalid_calls_fail_before_touching_a_device():
+    lib = _native.load()
+    rc = lib.r3c_conv3d_fwd(None, None, None, None, None, None, 0, None)
+    assert rc == _native.R3C_INVALID
+    assert b"NULL" in lib.r3c_last_error()
+    bad = _desc(k=5, pad=2)
+    assert lib.r3c_conv3d_dw(ctypes.byref(bad), None, None, None, 2, None, 2, None, 0, None) == _native.R3C_UNSUPPORTED
+    assert b"kernel 5" in lib.r3c_last_error()
+
+
+@pytest.mark.parametrize("k,pad", [(3, 1), (3, 0), (1, 0), (1, 2)])
+def test_dw_workspace_scales_with_problem(k, pad):
+    lib = _native.load()
+    small = lib.r3c_conv3d_dw_workspace(ctypes.byref(_desc(k=k, pad=pad, sp=(4, 4, 16))))
+    big = lib.r3c_conv3d_dw_workspace(ctypes.byref(_desc(k=k, pad=pad, sp=(32, 64, 64))))
+    assert 0 < small <= big <= (96 << 20) + (1 << 20)
