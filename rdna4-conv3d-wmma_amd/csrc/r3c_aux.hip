@@ -5,10 +5,10 @@
 
 namespace r3c {
 
-// Packed layout: [chunk][step][colblock][lane][8], lane = 16 * g + j.  Lane
-// (g, j) of step s holds k group kg = 4 s + g = (tap, 8-channel group cg) and
-// column colblock * 16 + j, i.e. exactly the B operand the row kernel feeds to
-// v_mfma_f32_16x16x32.  Out-of-range k or columns are zero.
+// Packed layout: [chunk][step][colblock][lane][8], lane = 32 * g + j.  Lane
+// (g, j) of step s holds k group kg = 2 s + g = (tap, 8-channel group cg) and
+// column colblock * 32 + j, i.e. exactly the B operand the row kernel feeds to
+// v_mfma_f32_32x32x16.  Out-of-range k or columns are zero.
 //
 // Weight index maps (w is PyTorch's parameter layout):
 //   K1/K3 forward   : Conv3d w (Cout, Cin, t)      -> w[col][ci][tap]
@@ -29,14 +29,14 @@ __global__ void pack_weight_kernel(const PackArgs a) {
   rest /= a.nbt_pad;
   const int s = (int)(rest % a.nstep);
   const int chunk = (int)(rest / a.nstep);
-  const int g = lane >> 4, j = lane & 15;
+  const int g = lane >> 5, j = lane & 31;
   const int g8 = a.ck / 8;
-  const int kg = 4 * s + g;
+  const int kg = 2 * s + g;
   uint16_t v = 0;
   if (kg < a.taps * g8) {
     const int tap = kg / g8, cg = kg % g8;
     const int ci = chunk * a.ck + cg * 8 + e;
-    const int col = nb * 16 + j;
+    const int col = nb * 32 + j;
     if (ci < a.cs && col < a.ncols) {
       const int mode = a.mode & 15;
       const bool dx = (a.mode & 16) != 0;

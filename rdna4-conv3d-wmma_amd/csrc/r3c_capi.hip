@@ -18,29 +18,44 @@
 
 namespace r3c {
 
-bool launch_fwd_k3(int dtype, int ck, int nb, const FwdArgs& a, size_t lds, hipStream_t s);
-bool launch_fwd_k1(int dtype, int ck, int nb, const FwdArgs& a, size_t lds, hipStream_t s);
-bool launch_fwd_t2dx(int dtype, int ck, int nb, const FwdArgs& a, size_t lds, hipStream_t s);
-bool launch_fwd_t2fwd(int dtype, int ck, int nb, const FwdArgs& a, size_t lds, hipStream_t s);
-bool launch_wgrad_k3(int dtype, int fb, int cbw, const WgradArgs& a, size_t lds, hipStream_t s);
-bool launch_wgrad_k1(int dtype, int fb, int cbw, const WgradArgs& a, size_t lds, hipStream_t s);
-bool launch_wgrad_t2(int dtype, int fb, int cbw, const WgradArgs& a, size_t lds, hipStream_t s);
+#define R3C_DECL_ROW(m)                                                                       \
+  bool launch_row_##m##_bf16(int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s); \
+  bool launch_row_##m##_f16(int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s);
+R3C_DECL_ROW(k3)
+R3C_DECL_ROW(k1)
+R3C_DECL_ROW(t2dx)
+R3C_DECL_ROW(t2fwd)
+#undef R3C_DECL_ROW
+#define R3C_DECL_WG(m)                                                                    \
+  bool launch_wgrad_##m##_bf16(int cbw, const WgArgs& a, size_t lds, hipStream_t s); \
+  bool launch_wgrad_##m##_f16(int cbw, const WgArgs& a, size_t lds, hipStream_t s);
+R3C_DECL_WG(k3)
+R3C_DECL_WG(k1)
+R3C_DECL_WG(t2dw)
+#undef R3C_DECL_WG
 
-bool launch_igemm_fwd(int dtype, int mode, int ck, int nb, const FwdArgs& a, size_t lds, hipStream_t s) {
+bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s) {
+  const bool bf = dtype == R3C_BF16;
   switch (mode) {
-    case MODE_K3: return launch_fwd_k3(dtype, ck, nb, a, lds, s);
-    case MODE_K1: return launch_fwd_k1(dtype, ck, nb, a, lds, s);
-    case MODE_T2DX: return launch_fwd_t2dx(dtype, ck, nb, a, lds, s);
-    case MODE_T2FWD: return launch_fwd_t2fwd(dtype, ck, nb, a, lds, s);
+    case MODE_K3:
+      return bf ? launch_row_k3_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_k3_f16(nb, cl, wf, a, grid, lds, s);
+    case MODE_K1:
+      return bf ? launch_row_k1_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_k1_f16(nb, cl, wf, a, grid, lds, s);
+    case MODE_T2DX:
+      return bf ? launch_row_t2dx_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_t2dx_f16(nb, cl, wf, a, grid, lds, s);
+    case MODE_T2FWD:
+      return bf ? launch_row_t2fwd_bf16(nb, cl, wf, a, grid, lds, s)
+                : launch_row_t2fwd_f16(nb, cl, wf, a, grid, lds, s);
     default: return false;
   }
 }
 
-bool launch_igemm_wgrad(int dtype, int mode, int fb, int cbw, const WgradArgs& a, size_t lds, hipStream_t s) {
+bool launch_wgrad(int dtype, int mode, int cbw, const WgArgs& a, size_t lds, hipStream_t s) {
+  const bool bf = dtype == R3C_BF16;
   switch (mode) {
-    case MODE_K3: return launch_wgrad_k3(dtype, fb, cbw, a, lds, s);
-    case MODE_K1: return launch_wgrad_k1(dtype, fb, cbw, a, lds, s);
-    case MODE_T2DW: return launch_wgrad_t2(dtype, fb, cbw, a, lds, s);
+    case MODE_K3: return bf ? launch_wgrad_k3_bf16(cbw, a, lds, s) : launch_wgrad_k3_f16(cbw, a, lds, s);
+    case MODE_K1: return bf ? launch_wgrad_k1_bf16(cbw, a, lds, s) : launch_wgrad_k1_f16(cbw, a, lds, s);
+    case MODE_T2DW: return bf ? launch_wgrad_t2dw_bf16(cbw, a, lds, s) : launch_wgrad_t2dw_f16(cbw, a, lds, s);
     default: return false;
   }
 }
@@ -125,6 +140,7 @@ struct TimedLaunch {
 
 constexpr int64_t kMaxLds = 160 * 1024;
 constexpr int kWgTarget = 512;                 // weight-gradient workgroups to aim for
+constexpr int kNumCUs = 256;                   // MI355X compute units
 constexpr int64_t kMaxPartialBytes = 96ll << 20;
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -194,12 +210,22 @@ bool vec16_ok(const void* p, const int64_t* s) {
   return (s[0] % 8 == 0) && (s[2] % 8 == 0) && (s[3] % 8 == 0) && (s[4] % 8 == 0);
 }
 
+// Bytes of one sample reachable from its base through `strides` (0 if too large
+// for 32-bit buffer offsets).
+uint32_t sample_bytes(const int64_t* st, int c, int d, int h, int w) {
+  const int64_t last = (int64_t)(c - 1) * st[1] + (int64_t)(d - 1) * st[2] + (int64_t)(h - 1) * st[3] +
+                       (int64_t)(w - 1) * st[4];
+  const int64_t bytes = (last + 8) * 2;  // round up so a 16-byte load at the last element stays in range
+  if (bytes >= (int64_t)0x3fffffff) return 0;
+  return (uint32_t)bytes;
+}
+
 // ---------------------------------------------------------------------------
 // Row-kernel plan (Conv3d fwd / dX, ConvTranspose fwd / dX)
 // ---------------------------------------------------------------------------
-struct FwdPlan {
-  int mode, ck, nb, mb;
-  FwdArgs a;
+struct RowPlan {
+  int mode, ck, nb, cl;
+  RowArgs a;
   PackArgs pk;
   size_t lds;
   int64_t wpk_bytes;
@@ -220,12 +246,14 @@ int pick_blocks(int nbt, const int* opts, int nopt) {
   return best;
 }
 
-void pick_box(int rows, int Rd, int Rh, int halo, int& TD, int& TH) {
+// Box of `rows` 32-wide lines: TD x TH = rows, TD in [td_min, td_max], minimising
+// the padded, halo'd volume.
+void pick_box(int rows, int Rd, int Rh, int halo, int td_min, int td_max, int& TD, int& TH) {
   int64_t best = -1;
-  for (int td = 1; td <= rows; td *= 2) {
+  for (int td = td_min; td <= td_max && td <= rows; td *= 2) {
     const int th = rows / td;
     const int64_t cost = (int64_t)cdiv(Rd, td) * cdiv(Rh, th) * (td + halo) * (th + halo);
-    if (best < 0 || cost < best || (cost == best && td == 4)) {
+    if (best < 0 || cost < best || (cost == best && td == th)) {
       best = cost;
       TD = td;
       TH = th;
@@ -233,91 +261,85 @@ void pick_box(int rows, int Rd, int Rh, int halo, int& TD, int& TH) {
   }
 }
 
-void plan_fwd(const r3c_conv_desc* d, int op, FwdPlan& p) {
-  FwdArgs& a = p.a;
+void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
+  RowArgs& a = p.a;
   memset(&a, 0, sizeof a);
   const int k = d->kernel;
-  int cs = 0;
-  if (op == OP_CONV_FWD || op == OP_CONV_DX) {
-    p.mode = k == 3 ? MODE_K3 : MODE_K1;
-  } else {
-    p.mode = op == OP_T2_FWD ? MODE_T2FWD : MODE_T2DX;
-  }
+  int cs = 0, sc = 0, sdd = 0, sh = 0, sw = 0;
+  if (op == OP_CONV_FWD || op == OP_CONV_DX) p.mode = k == 3 ? MODE_K3 : MODE_K1;
+  else p.mode = op == OP_T2_FWD ? MODE_T2FWD : MODE_T2DX;
   switch (op) {
     case OP_CONV_FWD:
-      cs = d->cin;
-      a.Sd = d->d; a.Sh = d->h; a.Sw = d->w;
+      cs = d->cin; sdd = d->d; sh = d->h; sw = d->w;
       a.Rd = d->od; a.Rh = d->oh; a.Rw = d->ow;
-      a.Dd = d->od; a.Dh = d->oh; a.Dw = d->ow;
       a.pd = d->pad_d; a.ph = d->pad_h; a.pw = d->pad_w;
       a.ncols = d->cout;
       memcpy(a.ss, d->x_strides, sizeof a.ss);
       memcpy(a.sd, d->y_strides, sizeof a.sd);
       break;
     case OP_CONV_DX:
-      cs = d->cout;
-      a.Sd = d->od; a.Sh = d->oh; a.Sw = d->ow;
+      cs = d->cout; sdd = d->od; sh = d->oh; sw = d->ow;
       a.Rd = d->d; a.Rh = d->h; a.Rw = d->w;
-      a.Dd = d->d; a.Dh = d->h; a.Dw = d->w;
       a.pd = k - 1 - d->pad_d; a.ph = k - 1 - d->pad_h; a.pw = k - 1 - d->pad_w;
       a.ncols = d->cin;
       memcpy(a.ss, d->y_strides, sizeof a.ss);
       memcpy(a.sd, d->x_strides, sizeof a.sd);
       break;
     case OP_T2_FWD:
-      cs = d->cin;
-      a.Sd = d->d; a.Sh = d->h; a.Sw = d->w;
+      cs = d->cin; sdd = d->d; sh = d->h; sw = d->w;
       a.Rd = d->d; a.Rh = d->h; a.Rw = d->w;
-      a.Dd = d->od; a.Dh = d->oh; a.Dw = d->ow;
       a.ncols = 8 * d->cout;
       a.cout_t2 = d->cout;
       memcpy(a.ss, d->x_strides, sizeof a.ss);
       memcpy(a.sd, d->y_strides, sizeof a.sd);
       break;
     default:  // OP_T2_DX
-      cs = d->cout;
-      a.Sd = d->od; a.Sh = d->oh; a.Sw = d->ow;
+      cs = d->cout; sdd = d->od; sh = d->oh; sw = d->ow;
       a.Rd = d->d; a.Rh = d->h; a.Rw = d->w;
-      a.Dd = d->d; a.Dh = d->h; a.Dw = d->w;
       a.ncols = d->cin;
       memcpy(a.ss, d->y_strides, sizeof a.ss);
       memcpy(a.sd, d->x_strides, sizeof a.sd);
       break;
   }
+  (void)sc;
   a.Cs = cs;
-  p.ck = pick_ck(cs);
-  const int nbt = cdiv(a.ncols, 16);
-  if (p.mode == MODE_T2FWD) {
-    static const int opts[] = {8, 4, 2};
-    p.nb = pick_blocks(nbt, opts, 3);
-  } else {
-    static const int opts[] = {4, 3, 2, 1};
-    p.nb = pick_blocks(nbt, opts, 4);
-  }
-  p.mb = p.mode == MODE_T2DX ? 2 : 4;
-  const int rows = 4 * p.mb;
-  const int halo = p.mode == MODE_K3 ? 2 : 0;
-  pick_box(rows, a.Rd, a.Rh, halo, a.TD, a.TH);
+  a.Sd = sdd; a.Sh = sh; a.Sw = sw;
+  a.src_bytes = sample_bytes(a.ss, cs, sdd, sh, sw);
+  // Channel-contiguous sources are staged by direct-to-LDS 16-byte loads;
+  // others by 8 scalar loads per slot through registers.
+  p.cl = (a.ss[1] == 1 && cs % 8 == 0 && a.ss[0] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 &&
+          a.ss[4] % 8 == 0) ? 1 : 0;
+  const int taps_k = p.mode == MODE_K3 ? 27 : (p.mode == MODE_T2DX ? 8 : 1);
+  const int g8 = taps_k == 1 ? 2 : 1;
+  p.ck = 8 * g8;
+  const int nbt = cdiv(a.ncols, 32);
+  static const int opts[] = {3, 2, 1};
+  p.nb = pick_blocks(nbt, opts, 3);
+  const int rows = p.mode == MODE_T2DX ? 4 : 8;  // 4 waves x MB row blocks
+  if (p.mode == MODE_K3) pick_box(rows, a.Rd, a.Rh, 2, 2, 4, a.TD, a.TH);
+  else pick_box(rows, a.Rd, a.Rh, 0, 1, rows, a.TD, a.TH);
   a.nbd = cdiv(a.Rd, a.TD);
   a.nbh = cdiv(a.Rh, a.TH);
-  a.nbw = cdiv(a.Rw, 16);
+  a.nbw = cdiv(a.Rw, 32);
   a.n_ctiles = cdiv(nbt, p.nb);
   a.nbt_pad = a.n_ctiles * p.nb;
   a.nchunks = cdiv(cs, p.ck);
+  int hw;
   if (p.mode == MODE_K3) {
-    a.HD = a.TD + 2; a.HH = a.TH + 2; a.HW = 18;
+    a.HD = a.TD + 2; a.HH = a.TH + 2; hw = 34;
   } else if (p.mode == MODE_T2DX) {
-    a.HD = 2 * a.TD; a.HH = 2 * a.TH; a.HW = 32;
+    a.HD = 2 * a.TD; a.HH = 2 * a.TH; hw = 64;
   } else {
-    a.HD = a.TD; a.HH = a.TH; a.HW = 16;
+    a.HD = a.TD; a.HH = a.TH; hw = 32;
   }
-  const int g8 = p.ck / 8;
-  const int cp = (g8 & 1) ? p.ck : p.ck + 8;
-  const int taps = p.mode == MODE_K3 ? 27 : (p.mode == MODE_T2DX ? 8 : 1);
-  const int nstep = cdiv(taps * g8, 4);
-  const int64_t hpos = (int64_t)a.HD * a.HH * a.HW;
-  p.lds = (size_t)(hpos * cp * 2 + nstep * 4 * 4);
-  a.nblocks = 0;  // filled with the batch at launch
+  const int hpos = a.HD * a.HH * hw;
+  a.CGS = (hpos + 255) / 256 * 256;
+  const int taps = taps_k;
+  const int nstep = cdiv(taps * g8, 2);
+  const int64_t wchunk = (int64_t)nstep * p.nb * 1024;  // bytes of one chunk's fragments
+  a.wfull = (a.n_ctiles == 1 && wchunk * a.nchunks <= 48 * 1024) ? 1 : 0;
+  const int64_t wbytes = a.wfull ? wchunk * a.nchunks : 2 * wchunk;
+  p.lds = (size_t)(2 * g8 * a.CGS * 16 + wbytes + 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4 + (int64_t)nstep * 2 * 4);
   PackArgs& pk = p.pk;
   memset(&pk, 0, sizeof pk);
   pk.cs = cs;
@@ -334,11 +356,12 @@ void plan_fwd(const r3c_conv_desc* d, int op, FwdPlan& p) {
   p.wpk_bytes = pk.total * 2;
 }
 
-int run_fwd(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
+int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
             int64_t ws_bytes, void* stream) {
-  FwdPlan p;
-  plan_fwd(d, op, p);
+  RowPlan p;
+  plan_row(d, op, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
+  if (p.a.src_bytes == 0) return fail(R3C_UNSUPPORTED, "one input sample exceeds 1 GiB (32-bit buffer offsets)");
   if (ws_bytes < align256(p.wpk_bytes))
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes,
                 (long long)align256(p.wpk_bytes));
@@ -356,20 +379,24 @@ int run_fwd(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   }
   rc = check_launch("weight pack");
   if (rc) return rc;
-  FwdArgs a = p.a;
+  RowArgs a = p.a;
   a.src = static_cast<const uint16_t*>(src);
   a.wpk = static_cast<const uint16_t*>(ws);
   a.bias = static_cast<const uint16_t*>(bias);
   a.dst = static_cast<uint16_t*>(dst);
-  a.src_cl = vec16_ok(src, a.ss) ? 1 : 0;
-  const int64_t blocks = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
-  if (blocks >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
-  a.nblocks = (int32_t)blocks;
+  a.src_cl = p.cl;
+  if (p.cl && (reinterpret_cast<uintptr_t>(src) & 15) != 0) return fail(R3C_INVALID, "source not 16-byte aligned");
+  const int64_t jobs = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
+  if (jobs >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
+  a.njobs = (int32_t)jobs;
+  const int per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(4, kMaxLds / (int64_t)std::max<size_t>(p.lds, 1)));
+  const int grid = (int)std::min<int64_t>(jobs, (int64_t)kNumCUs * per_cu);
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = launch_igemm_fwd(d->dtype, p.mode, p.ck, p.nb, a, p.lds, s);
+  const bool launched = launch_row(d->dtype, p.mode, p.nb, p.cl, a.wfull, a, grid, p.lds, s);
   tl.end();
   if (!launched)
-    return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d", p.mode, p.ck, p.nb);
+    return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d cl %d", p.mode, p.ck, p.nb,
+                p.cl);
   return check_launch("row kernel");
 }
 
@@ -377,16 +404,14 @@ int run_fwd(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // Weight-gradient plan (Conv3d dW k1/k3, ConvTranspose dW)
 // ---------------------------------------------------------------------------
 struct WgPlan {
-  int mode, fb, cbw, taps;
-  WgradArgs a;
+  int mode, cbw, taps;
+  WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes;
 };
 
-int pad16(int c) { return (c / 16) % 2 == 0 ? c + 16 : c; }  // LDS row pitch: an odd number of 32-byte units
-
 void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
-  WgradArgs& a = p.a;
+  WgArgs& a = p.a;
   memset(&a, 0, sizeof a);
   if (transpose) {
     p.mode = MODE_T2DW;
@@ -406,82 +431,40 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
     memcpy(a.fs, d->y_strides, sizeof a.fs);
     memcpy(a.gs, d->x_strides, sizeof a.gs);
   }
-  const int nfb = cdiv(a.Fc, 16), ngb = cdiv(a.Gc, 16);
-  // F blocks per workgroup.
-  {
-    static const int opts[] = {3, 2, 1};
-    p.fb = nfb <= 3 ? nfb : pick_blocks(nfb, opts, 3);
-  }
-  // Column tiling: (CBW, GCB) maximising useful MFMA slots.
-  int cbw_opts[3];
-  int ncbw = 0;
-  if (p.mode == MODE_K3) {
-    if (p.fb == 3) {
-      cbw_opts[0] = 7;
-      ncbw = 1;
-    } else {
-      cbw_opts[0] = 14;
-      cbw_opts[1] = 7;
-      ncbw = 2;
-    }
-  } else if (p.mode == MODE_K1) {
-    cbw_opts[0] = 1;
-    ncbw = 1;
-  } else {
-    cbw_opts[0] = 7;
-    cbw_opts[1] = 4;
-    cbw_opts[2] = 2;
-    ncbw = 3;
-  }
-  double best_eff = -1.0;
-  int best_tiles = 0;
-  const int gcb_max = p.mode == MODE_K1 ? 4 : 3;
-  for (int i = 0; i < ncbw; ++i) {
-    for (int gcb = 1; gcb <= gcb_max; ++gcb) {
-      const int slots = 4 * cbw_opts[i];
-      if (gcb > slots) continue;
-      const int tt = std::min(p.taps, slots / gcb);
-      const int ntt = cdiv(p.taps, tt);
-      const int ngt = cdiv(ngb, gcb);
-      const double eff = (double)p.taps * ngb / ((double)ntt * ngt * slots);
-      const int tiles = ntt * ngt;
-      if (eff > best_eff + 1e-9 || (eff > best_eff - 1e-9 && tiles < best_tiles)) {
-        best_eff = eff;
-        best_tiles = tiles;
-        p.cbw = cbw_opts[i];
-        a.GCB = gcb;
-        a.TT = tt;
-      }
-    }
-  }
-  a.n_ftiles = cdiv(nfb, p.fb);
-  a.n_gtiles = cdiv(ngb, a.GCB);
-  a.n_ttiles = cdiv(p.taps, a.TT);
-  a.Fpad = a.n_ftiles * p.fb * 16;
-  a.Gpad = a.n_gtiles * a.GCB * 16;
-  a.cpf = pad16(p.fb * 16);
-  a.cpg = pad16(a.GCB * 16);
+  a.f_bytes = sample_bytes(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
+  a.g_bytes = sample_bytes(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
+  // G channel range per tile: a multiple of 8 (16-byte staging) and of 4 (quads).
+  if (a.Gc <= 32) a.GCW = (a.Gc + 7) / 8 * 8;
+  else if (a.Gc % 32 == 0) a.GCW = 32;
+  else if (a.Gc % 24 == 0) a.GCW = 24;
+  else a.GCW = 32;
+  a.n_ftiles = cdiv(a.Fc, 32);
+  a.n_gtiles = cdiv(a.Gc, a.GCW);
+  a.Fpad = a.n_ftiles * 32;
+  a.Gpad = a.n_gtiles * a.GCW;
+  const int ncb = cdiv((int64_t)p.taps * (a.GCW / 4), 8);
+  p.cbw = cdiv(ncb, 4);
+  const int cbw_max = p.mode == MODE_K3 ? 7 : (p.mode == MODE_K1 ? 2 : 4);
+  if (p.cbw > cbw_max) p.cbw = cbw_max;  // cannot happen with GCW <= 32
+  // Box: TD x TH x 16 positions.
   if (p.mode == MODE_K3) {
     a.TD = 2; a.TH = 4;
+    if ((int64_t)256 * 32 * 2 + (int64_t)6 * 6 * 18 * a.GCW * 2 <= 50 * 1024) { a.TD = 4; a.TH = 4; }
+    a.HD = a.TD + 2; a.HH = a.TH + 2; a.HW = 18;
   } else if (p.mode == MODE_K1) {
     a.TD = 4; a.TH = 4;
+    a.HD = a.TD; a.HH = a.TH; a.HW = 16;
   } else {
     a.TD = 2; a.TH = 2;
+    a.HD = 2 * a.TD; a.HH = 2 * a.TH; a.HW = 32;
   }
   a.th_log2 = a.TH == 1 ? 0 : (a.TH == 2 ? 1 : (a.TH == 4 ? 2 : 3));
-  if (p.mode == MODE_K3) {
-    a.HD = a.TD + 2; a.HH = a.TH + 2; a.HW = 18;
-  } else if (p.mode == MODE_T2DW) {
-    a.HD = 2 * a.TD; a.HH = 2 * a.TH; a.HW = 32;
-  } else {
-    a.HD = a.TD; a.HH = a.TH; a.HW = 16;
-  }
   a.nbd = cdiv(a.Rd, a.TD);
   a.nbh = cdiv(a.Rh, a.TH);
   a.nbw = cdiv(a.Rw, 16);
   const int64_t nbox = (int64_t)d->n * a.nbd * a.nbh * a.nbw;
   a.nbox = (int32_t)std::min<int64_t>(nbox, (1ll << 31) - 1);
-  const int tiles = a.n_ftiles * a.n_gtiles * a.n_ttiles;
+  const int tiles = a.n_ftiles * a.n_gtiles;
   const int64_t per_split = (int64_t)a.Fpad * p.taps * a.Gpad * 4;
   int64_t nsplit = cdiv(kWgTarget, tiles);
   nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
@@ -490,7 +473,7 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   a.nblocks = (int32_t)(nsplit * tiles);
   const int64_t boxpos = (int64_t)a.TD * a.TH * 16;
   const int64_t hpos = (int64_t)a.HD * a.HH * a.HW;
-  p.lds = (size_t)(boxpos * a.cpf * 2 + hpos * a.cpg * 2);
+  p.lds = (size_t)(boxpos * 32 * 2 + hpos * a.GCW * 2);
   p.part_bytes = align256(nsplit * per_split);
   p.dbpart_bytes = align256(nsplit * (int64_t)std::max(a.Fpad, p.taps * a.Gpad) * 4);
 }
@@ -500,6 +483,8 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   WgPlan p;
   plan_wgrad(d, transpose, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
+  if (p.a.f_bytes == 0 || p.a.g_bytes == 0)
+    return fail(R3C_UNSUPPORTED, "one sample exceeds 1 GiB (32-bit buffer offsets)");
   if (ws_bytes < p.part_bytes + p.dbpart_bytes)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes,
                 (long long)(p.part_bytes + p.dbpart_bytes));
@@ -510,19 +495,18 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   int rc = check_device();
   if (rc) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  WgradArgs a = p.a;
+  WgArgs a = p.a;
   a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
-  a.f_cl = vec16_ok(a.fsrc, a.fs) ? 1 : 0;
-  a.g_cl = vec16_ok(a.gsrc, a.gs) ? 1 : 0;
+  a.f_cl = (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0) ? 1 : 0;
+  a.g_cl = (vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0) ? 1 : 0;
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
   TimedLaunch tl(KIND_WGRAD, s);
-  const bool launched = launch_igemm_wgrad(d->dtype, p.mode, p.fb, p.cbw, a, p.lds, s);
+  const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, a, p.lds, s);
   tl.end();
-  if (!launched)
-    return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d fb %d cbw %d", p.mode, p.fb, p.cbw);
+  if (!launched) return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d cbw %d", p.mode, p.cbw);
   rc = check_launch("weight-gradient kernel");
   if (rc) return rc;
   ReduceArgs r;
@@ -550,8 +534,8 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
 
 int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
-  FwdPlan p;
-  plan_fwd(d, op, p);
+  RowPlan p;
+  plan_row(d, op, p);
   return align256(p.wpk_bytes);
 }
 
@@ -598,14 +582,14 @@ int32_t r3c_conv3d_fwd(const r3c_conv_desc* d, const void* x, const void* w, con
                        int64_t ws_bytes, void* stream) {
   int rc = validate(d, false);
   if (rc) return rc;
-  return run_fwd(d, OP_CONV_FWD, x, w, bias, y, ws, ws_bytes, stream);
+  return run_row(d, OP_CONV_FWD, x, w, bias, y, ws, ws_bytes, stream);
 }
 
 int32_t r3c_conv3d_dx(const r3c_conv_desc* d, const void* dy, const void* w, void* dx, void* ws, int64_t ws_bytes,
                       void* stream) {
   int rc = validate(d, false);
   if (rc) return rc;
-  return run_fwd(d, OP_CONV_DX, dy, w, nullptr, dx, ws, ws_bytes, stream);
+  return run_row(d, OP_CONV_DX, dy, w, nullptr, dx, ws, ws_bytes, stream);
 }
 
 int32_t r3c_conv3d_dw(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype, void* db,
@@ -619,14 +603,14 @@ int32_t r3c_convt_k2s2_fwd(const r3c_conv_desc* d, const void* x, const void* w,
                            int64_t ws_bytes, void* stream) {
   int rc = validate(d, true);
   if (rc) return rc;
-  return run_fwd(d, OP_T2_FWD, x, w, bias, y, ws, ws_bytes, stream);
+  return run_row(d, OP_T2_FWD, x, w, bias, y, ws, ws_bytes, stream);
 }
 
 int32_t r3c_convt_k2s2_dx(const r3c_conv_desc* d, const void* dy, const void* w, void* dx, void* ws,
                           int64_t ws_bytes, void* stream) {
   int rc = validate(d, true);
   if (rc) return rc;
-  return run_fwd(d, OP_T2_DX, dy, w, nullptr, dx, ws, ws_bytes, stream);
+  return run_row(d, OP_T2_DX, dy, w, nullptr, dx, ws, ws_bytes, stream);
 }
 
 int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype,

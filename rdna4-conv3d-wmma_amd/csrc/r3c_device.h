@@ -22,7 +22,11 @@ namespace r3c {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+// Plain 128-bit vector: copies of it are register moves, never memcpy through
+// private memory (which a copy of the uint4 struct can turn into).
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 enum { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };

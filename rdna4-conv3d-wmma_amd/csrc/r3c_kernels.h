@@ -1,23 +1,20 @@
 // r3c_kernels.h -- kernel argument blocks and host-side launchers.
 //
-// Two kernel families cover the whole hot path:
+// Two kernel families cover the whole hot path, both on v_mfma_f32_32x32x16:
 //
-//  * igemm_fwd  ("row" GEMM): C[row position][column] = sum_k A[row][k] B[k][col]
-//      rows    = positions of a TD x TH x 16 box of the row grid
+//  * row kernel (r3c_row.h): C[row position][column] = sum_k A[row][k] B[k][col]
+//      rows    = positions of a TD x TH x 32 box of the row grid
 //      k       = (tap, source channel), walked in 8-channel groups
 //      columns = destination channels (or (tap, Cout) for ConvTranspose fwd)
 //    Modes: K3 / K1 (Conv3d fwd and dX), T2DX (ConvTranspose dX), T2FWD
-//    (ConvTranspose fwd, scatter epilogue).  The source box plus halo is staged
-//    once per channel chunk into LDS as [position][channel]; the weight arrives
-//    pre-packed in MFMA fragment order.
+//    (ConvTranspose fwd, scatter epilogue).
 //
-//  * igemm_wgrad ("reduction" GEMM): C[f][(tap, g)] = sum_pos F[pos][f] G[pos (+) tap][g]
+//  * weight-gradient kernel (r3c_wgrad.h): C[f][(tap, g)] = sum_pos F[pos][f] G[pos (+) tap][g]
 //      K = positions (the huge N*D*H*W axis), split deterministically into
 //      `nsplit` contiguous box ranges; every split writes fp32 partials that a
-//      second kernel sums in a fixed order.  Both operands come from
-//      [position][channel] LDS tiles through ds_read_tr16_b64.
-//    Modes: K3 / K1 (Conv3d dW: F = dY, G = X) and T2 (ConvTranspose dW:
-//    F = X, G = dY at 2p + tap).
+//      second kernel sums in a fixed order.
+//    Modes: K3 / K1 (Conv3d dW: F = dY, G = x) and T2DW (ConvTranspose dW:
+//    F = x, G = dY at 2p + tap).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -26,35 +23,38 @@ namespace r3c {
 
 enum Mode { MODE_K1 = 0, MODE_K3 = 1, MODE_T2DX = 2, MODE_T2FWD = 3, MODE_T2DW = 4 };
 
-struct FwdArgs {
+struct RowArgs {
   const uint16_t* src;   // x (fwd) or dy (dX)
   const uint16_t* wpk;   // packed fragments [chunk][step][colblock][lane][8]
   const uint16_t* bias;  // may be null
   uint16_t* dst;
   int64_t ss[5];         // source strides (n, c, d, h, w)
   int64_t sd[5];         // destination strides (n, c, d, h, w)
+  uint32_t src_bytes;    // bytes of one source sample reachable from its base (buffer range)
   int32_t Cs, Sd, Sh, Sw;  // source channels and spatial dims
   int32_t Rd, Rh, Rw;      // row grid (destination grid; source grid for T2FWD)
-  int32_t Dd, Dh, Dw;      // destination spatial dims
   int32_t pd, ph, pw;      // Conv3d padding (K1/K3)
-  int32_t TD, TH;          // box = TD x TH x 16 rows of the row grid
+  int32_t TD, TH;          // box = TD x TH x 32 rows of the row grid
   int32_t nbd, nbh, nbw;   // boxes per dimension
   int32_t n_ctiles;        // column tiles of NB blocks
   int32_t nbt_pad;         // column blocks in the packed weight (n_ctiles * NB)
   int32_t nchunks;         // source-channel chunks of CK
   int32_t ncols;           // real columns (Cd, or 8 * Cout for T2FWD)
   int32_t cout_t2;         // T2FWD: Cout, to split a column into (tap, channel)
-  int32_t HD, HH, HW;      // LDS tile dims (box + halo, or 2 x box for T2DX)
+  int32_t HD, HH;          // LDS tile dims (the w extent is fixed per mode)
+  int32_t CGS;             // 16-byte slots per activation buffer (HD*HH*HW rounded up to 256)
+  int32_t wfull;           // 1: every chunk's weights stay resident in LDS
   int32_t src_cl;          // 1: channel-contiguous 16-byte source loads are legal
-  int32_t nblocks;         // total workgroups (grid size)
+  int32_t njobs;           // (box, column tile) jobs; workgroups stride over them
 };
 
-struct WgradArgs {
+struct WgArgs {
   const uint16_t* fsrc;  // F operand tensor (dY for Conv3d, x for ConvTranspose)
   const uint16_t* gsrc;  // G operand tensor (x for Conv3d, dY for ConvTranspose)
   float* part;           // [nsplit][Fpad][TAPS][Gpad] fp32 partials
   float* dbpart;         // [nsplit][Fpad] (db from F) or [nsplit][TAPS][Gpad] (db from G)
   int64_t fs[5], gs[5];
+  uint32_t f_bytes, g_bytes;  // per-sample buffer ranges
   int32_t Fc, Gc;          // channel counts
   int32_t Rd, Rh, Rw;      // F (row) grid
   int32_t Gd, Gh, Gw;      // G grid
@@ -62,13 +62,12 @@ struct WgradArgs {
   int32_t TD, TH, th_log2; // box = TD x TH x 16 positions; TH is a power of two
   int32_t nbd, nbh, nbw, nbox;
   int32_t nsplit;
-  int32_t n_ftiles, n_gtiles, n_ttiles;
-  int32_t GCB, TT;         // G blocks and taps per column tile
+  int32_t n_ftiles, n_gtiles;
+  int32_t GCW;             // G channels per tile (multiple of 8)
   int32_t Fpad, Gpad;
   int32_t HD, HH, HW;      // G tile dims
   int32_t f_cl, g_cl;      // channel-contiguous 16-byte loads legal
   int32_t db_mode;         // 0 none, 1 db = sum over F, 2 db = sum over G
-  int32_t cpf, cpg;        // LDS row pitches (elements)
   int32_t nblocks;
 };
 
@@ -96,10 +95,9 @@ struct PackArgs {
 };
 
 // Host launchers (return false when no instantiation matches).
-bool launch_igemm_fwd(int dtype, int mode, int ck, int nb, const FwdArgs& a, size_t lds_bytes,
-                      hipStream_t stream);
-bool launch_igemm_wgrad(int dtype, int mode, int fb, int cbw, const WgradArgs& a, size_t lds_bytes,
-                        hipStream_t stream);
+bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds_bytes,
+                hipStream_t stream);
+bool launch_wgrad(int dtype, int mode, int cbw, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 

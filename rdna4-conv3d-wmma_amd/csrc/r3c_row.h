@@ -1,0 +1,438 @@
+// r3c_row.h -- implicit-GEMM "row" kernel for gfx950 on v_mfma_f32_32x32x16 (template body).
+//
+//   C[row position][column] = sum_k A[row][k] * B[k][column]
+//
+// A workgroup (4 waves) owns a box of TD x TH x 32 positions of the row grid
+// and NB column blocks of 32.  Wave w owns MB row blocks; a row block is one
+// 32-wide line along w, so MFMA row i is position w0 + i.
+//
+// Operand layouts (measured on gfx950, lane l, g = l / 32, i = l % 32):
+//   A (32 x 16): lane holds A[i][8g .. 8g+7]
+//   B (16 x 32): lane holds B[8g .. 8g+7][i]
+//   C (32 x 32): acc[4q + r] = C[8q + 4g + r][i]
+//
+// K walks (tap, 8-channel group); one MFMA consumes two groups (g = 0, 1).
+// Per source-channel chunk of CK channels, the box plus its halo is staged into
+// LDS as [channel group][position] 16-byte slots (8 channels of one position).
+// An A fragment is then one ds_read_b128 per lane at slot (cg, row + tap): the
+// 32 lanes of a half-wave read 32 consecutive slots, so lanes l and l+16 sit
+// 256 B apart and each 16-lane group covers 16 distinct slots -- the pattern
+// gfx950's LDS serves at full rate.  ConvTranspose dX stores even and odd w
+// of the 2x-wide dY box in separate halves of each row so its stride-2 taps
+// read consecutive slots as well.  B fragments are 16-byte loads of the weight
+// pre-packed in lane order.
+//
+// Loads go through a buffer resource with 32-bit offsets: out-of-range
+// positions (the zero padding) use an offset past num_records, which the
+// hardware returns as zero, so there are no bounds branches.
+//
+// Index math follows the reference kernels: K3 fwd (src/rdna4_conv3d/
+// conv3d_wmma.py:372-444), K1 fwd (328-369), ConvTranspose fwd scatter
+// (793-860) and ConvTranspose dX gather (863-931).
+#pragma once
+#include "r3c_device.h"
+#include "r3c_kernels.h"
+
+namespace r3c {
+
+// n / d for n < 4096 and 1 <= d < 256, via a 20-bit reciprocal (exact in range).
+struct FastDiv20 {
+  uint32_t m;
+  __device__ __forceinline__ explicit FastDiv20(uint32_t d) : m(((1u << 20) + d - 1) / d) {}
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return (n * m) >> 20; }
+};
+
+constexpr int kOob = 0x7fffff00;  // byte offset past any num_records: the load returns 0
+
+template <int MODE>
+struct RowGeom {
+  static constexpr int TAPS = MODE == MODE_K3 ? 27 : (MODE == MODE_T2DX ? 8 : 1);
+  static constexpr int HW = MODE == MODE_K3 ? 34 : (MODE == MODE_T2DX ? 64 : 32);
+  // Row blocks (32 positions) per wave, and the largest LDS tile any allowed box
+  // needs (K3: 2x4 or 4x2 boxes plus halo; T2DX: boxes of 4 rows, 2x in dY).
+  static constexpr int MB = MODE == MODE_T2DX ? 1 : 2;
+  static constexpr int MAXHPOS = MODE == MODE_K3 ? 4 * 6 * 34 : (MODE == MODE_T2DX ? 16 * 64 : 8 * 32);
+  // A chunk is G8 8-channel groups: one group per tap when there are taps, two
+  // for the single-tap modes so an MFMA step (two groups) carries no padding.
+  static constexpr int G8 = TAPS == 1 ? 2 : 1;
+  static constexpr int NSTEP = (TAPS * G8 + 1) / 2;
+  static constexpr int MAXK = (MAXHPOS + 255) / 256;  // staging slots per thread per group
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename T>
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const f32x16_t& c);
+template <>
+__device__ __forceinline__ f32x16_t mfma32<bf16_tag>(const uint4& a, const uint4& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16_t mfma32<f16_tag>(const uint4& a, const uint4& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                0, 0, 0);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Half k of element q of a uint4 (q in 0..7), without taking its address.
+__device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
+  const uint32_t w = q < 2 ? v.x : (q < 4 ? v.y : (q < 6 ? v.z : v.w));
+  return (uint16_t)((q & 1) ? (w >> 16) : (w & 0xffff));
+}
+
+// LDS: act[2][G8][HPAD] 16-byte slots (double-buffered tile, HPAD = HPOS rounded
+// up to 256), the weight fragments (all of K when WF, else two chunk buffers of
+// NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB), the bias
+// table (fp32, one per packed column) and the tap table.
+//
+// Pipeline: one stage = one 8-channel (16 for single-tap modes) chunk of one
+// job.  Stage t+1's activations (and, without WF, its weights) are loaded into
+// registers while stage t computes from LDS, then written to the other buffer;
+// one barrier per stage.  Only the resident weights (WF) use direct-to-LDS
+// loads, once, before the loop: the compiler makes every LDS read that follows
+// an in-flight direct-to-LDS load wait for it, which would serialise a
+// per-stage DMA with the compute it is meant to overlap.
+//
+// Epilogue: a wave converts each 32 x 32 C tile (plus bias) to 16-bit and
+// writes it to its scratch as [column][position] with 8-byte writes, then
+// reads it back in store order -- 8 consecutive positions of one channel per
+// lane when positions are contiguous in memory (NCDHW), or, through
+// ds_read_tr16_b64, 8 consecutive channels of one position per lane when
+// channels are contiguous (NDHWC) -- so every global store is 16 bytes.
+template <typename T, int MODE, int NB, int CL, int WF>
+__global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
+  extern __shared__ uint4 smem4[];
+  constexpr int TAPS = RowGeom<MODE>::TAPS;
+  constexpr int HW = RowGeom<MODE>::HW;
+  constexpr int MB = RowGeom<MODE>::MB;
+  constexpr int NSTEP = RowGeom<MODE>::NSTEP;
+  constexpr int MAXK = RowGeom<MODE>::MAXK;
+  constexpr int G8 = RowGeom<MODE>::G8;
+  constexpr int WFRAG = NSTEP * NB * 64;              // uint4 per chunk of weights
+  constexpr int WIT = WF ? 1 : (WFRAG + 255) / 256;   // weight uint4 per thread per chunk
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int g = lane >> 5;
+  const int li = lane & 31;
+
+  const int HH = a.HH;
+  const int HPOS = a.HD * HH * HW;
+  const int HPAD = a.CGS;  // HPOS rounded up to a multiple of 256
+  const int ABUF = G8 * HPAD;  // slots per activation buffer
+  uint4* act = smem4;
+  uint4* wts = smem4 + 2 * ABUF;
+  const int wslots = WF ? a.nchunks * WFRAG : 2 * WFRAG;
+  uint16_t* scr = reinterpret_cast<uint16_t*>(wts + wslots) + wv * 1024;
+  float* btab = reinterpret_cast<float*>(wts + wslots + 4 * 128);
+  const int nbcol = a.nbt_pad * 32;
+  int* ktab = reinterpret_cast<int*>(btab + nbcol);
+
+  // Contiguous job range of this workgroup; a job is (box, column tile).
+  const int j0 = (int)(((int64_t)blockIdx.x * a.njobs) / gridDim.x);
+  const int j1 = (int)(((int64_t)(blockIdx.x + 1) * a.njobs) / gridDim.x);
+  if (j0 >= j1) return;
+
+  for (int kg = tid; kg < NSTEP * 2; kg += 256) {
+    int off = 0;  // K padding: the row's own slot, times zero weights
+    if (kg < TAPS * G8) {
+      const int tap = kg / G8, cg = kg - (kg / G8) * G8;
+      if (MODE == MODE_K3) off = ((tap / 9) * HH + (tap / 3) % 3) * HW + tap % 3;
+      else if (MODE == MODE_T2DX) off = ((tap >> 2) * HH + ((tap >> 1) & 1)) * HW + (tap & 1) * 32;
+      off += cg * HPAD;
+    }
+    ktab[kg] = off;
+  }
+  for (int c = tid; c < nbcol; c += 256) {
+    float bv = 0.f;
+    if (a.bias && c < a.ncols) bv = to_f32<T>(a.bias[MODE == MODE_T2FWD ? c % a.cout_t2 : c]);
+    btab[c] = bv;
+  }
+
+  int rowbase[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int r = wv * MB + mb;
+    const int td = r / a.TH, th = r - (r / a.TH) * a.TH;
+    if (MODE == MODE_T2DX) rowbase[mb] = ((2 * td) * HH + 2 * th) * HW + li;
+    else rowbase[mb] = (td * HH + th) * HW + li;
+  }
+
+  // Staging slot k of this thread is tile position 256 k + tid.
+  int irel[MAXK];
+  {
+    const FastDiv20 divHH((uint32_t)HH);
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      const int hp = k * 256 + tid;
+      const int t = hp / HW;
+      int hw = hp - t * HW;
+      if (MODE == MODE_T2DX) hw = (hw & 31) * 2 + (hw >> 5);  // de-interleaved row: slot -> w
+      const int hd = (int)divHH.div((uint32_t)t);
+      const int hh = t - hd * HH;
+      irel[k] = hp < HPOS ? (hd | (hh << 8) | (hw << 16)) : -1;
+    }
+  }
+  const int ss1 = (int)a.ss[1], ss2 = (int)a.ss[2], ss3 = (int)a.ss[3], ss4 = (int)a.ss[4];
+  uint4 pfa[G8 * MAXK];
+  u32x4_t pfw[WIT];
+
+  auto box_of = [&](int job, int& n, int& bd, int& bh, int& bw) {
+    int b = job / a.n_ctiles;
+    bw = b % a.nbw;
+    b /= a.nbw;
+    bh = b % a.nbh;
+    b /= a.nbh;
+    bd = b % a.nbd;
+    n = b / a.nbd;
+  };
+  const uint4* wsrc = reinterpret_cast<const uint4*>(a.wpk);
+  // Issue the loads of stage (job, chunk) into registers.
+  auto issue = [&](int job, int chunk) {
+    int n, bd, bh, bw;
+    box_of(job, n, bd, bh, bw);
+    int s0d, s0h, s0w;
+    if (MODE == MODE_K3 || MODE == MODE_K1) {
+      s0d = bd * a.TD - a.pd;
+      s0h = bh * a.TH - a.ph;
+      s0w = bw * 32 - a.pw;
+    } else if (MODE == MODE_T2DX) {
+      s0d = 2 * bd * a.TD;
+      s0h = 2 * bh * a.TH;
+      s0w = 64 * bw;
+    } else {
+      s0d = bd * a.TD;
+      s0h = bh * a.TH;
+      s0w = bw * 32;
+    }
+    const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (int64_t)n * a.ss[0], a.src_bytes);
+#pragma unroll
+    for (int cg = 0; cg < G8; ++cg) {
+      const int c0 = chunk * 8 * G8 + cg * 8;
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k) {
+        const int r = irel[k];
+        const int gd = s0d + (r & 255), gh = s0h + ((r >> 8) & 255), gw = s0w + ((r >> 16) & 255);
+        const bool ok = r >= 0 && (unsigned)gd < (unsigned)a.Sd && (unsigned)gh < (unsigned)a.Sh &&
+                        (unsigned)gw < (unsigned)a.Sw && c0 < a.Cs;
+        const int off = 2 * (gd * ss2 + gh * ss3 + gw * ss4 + c0 * ss1);
+        if (CL) {
+          pfa[cg * MAXK + k] =
+              __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, ok ? off : kOob, 0, 0));
+        } else {
+          uint32_t wd[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(
+                src, (ok && c0 + 2 * q < a.Cs) ? off + 4 * q * ss1 : kOob, 0, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(
+                src, (ok && c0 + 2 * q + 1 < a.Cs) ? off + (4 * q + 2) * ss1 : kOob, 0, 0);
+            wd[q] = lo | (hi << 16);
+          }
+          pfa[cg * MAXK + k] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        }
+      }
+    }
+    if (!WF) {
+      const int ct = job % a.n_ctiles;
+#pragma unroll
+      for (int i = 0; i < WIT; ++i) {
+        // uint4 index inside the chunk's fragments; the tail of the last
+        // iteration re-reads the final fragment and is not committed.
+        const int e = i * 256 + tid < WFRAG ? i * 256 + tid : WFRAG - 1;
+        const int f = e >> 6, l = e & 63;
+        const int s = f / NB, nb = f - (f / NB) * NB;
+        pfw[i] = *reinterpret_cast<const u32x4_t*>(wsrc + (((size_t)chunk * NSTEP + s) * a.nbt_pad + ct * NB + nb) * 64 + l);
+      }
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int cg = 0; cg < G8; ++cg)
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k)
+        if (k * 256 < HPAD) act[buf * ABUF + cg * HPAD + k * 256 + tid] = pfa[cg * MAXK + k];
+    if (!WF) {
+#pragma unroll
+      for (int i = 0; i < WIT; ++i) {
+        const int e = i * 256 + tid;
+        if (e < WFRAG) *reinterpret_cast<u32x4_t*>(wts + buf * WFRAG + e) = pfw[i];
+      }
+    }
+  };
+
+  f32x16_t acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
+
+  if (WF) {  // every chunk's weights, once, straight into LDS
+    for (int c = 0; c < a.nchunks; ++c)
+      for (int f = wv; f < NSTEP * NB; f += 4) {
+        const int s = f / NB, nb = f - (f / NB) * NB;
+        const uint4* p = wsrc + (((size_t)c * NSTEP + s) * a.nbt_pad + nb) * 64 + lane;
+        __builtin_amdgcn_global_load_lds((const void*)p, (lds_void_t*)(wts + c * WFRAG + f * 64), 16, 0, 0);
+      }
+  }
+  int job = j0, chunk = 0, t = 0;
+  issue(job, 0);
+  while (true) {
+    const int buf = t & 1;
+    commit(buf);
+    __syncthreads();
+    int njob = job, nchunk = chunk + 1;
+    if (nchunk == a.nchunks) {
+      nchunk = 0;
+      ++njob;
+    }
+    const bool more = njob < j1;
+    if (more) issue(njob, nchunk);  // in flight while this stage computes
+
+    const int ct = job % a.n_ctiles;
+    const uint4* wc = WF ? wts + chunk * WFRAG : wts + buf * WFRAG;
+    const uint4* ab = act + buf * ABUF;
+#pragma unroll 2
+    for (int s = 0; s < NSTEP; ++s) {
+      const int koff = ktab[s * 2 + g];
+      uint4 bfr[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bfr[nb] = wc[(s * NB + nb) * 64 + lane];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const uint4 afr = ab[rowbase[mb] + koff];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr, bfr[nb], acc[mb][nb]);
+      }
+    }
+
+    if (chunk == a.nchunks - 1) {
+      // Epilogue: lane (g, i) holds rows 8q + 4g + r (w positions) of column i.
+      int n, bd, bh, bw;
+      box_of(job, n, bd, bh, bw);
+      const int r0d = bd * a.TD, r0h = bh * a.TH, r0w = bw * 32;
+      const int64_t* sd = a.sd;
+      uint16_t* dstn = a.dst + (int64_t)n * sd[0];
+      const bool pos_contig = sd[4] == 1;
+      const bool ch_contig = !pos_contig && sd[1] == 1;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int r = wv * MB + mb;
+        const int td = r / a.TH, th = r - (r / a.TH) * a.TH;
+        const int rd = r0d + td, rh = r0h + th;
+        if (rd < a.Rd && rh < a.Rh) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const int colbase = (ct * NB + nb) * 32;
+            if (colbase >= a.ncols) continue;
+            {  // C tile (+ bias) -> scratch [column][position]
+              const float bv = btab[colbase + li];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                uint2 v;
+                v.x = pack2(from_f32<T>(acc[mb][nb][4 * q + 0] + bv), from_f32<T>(acc[mb][nb][4 * q + 1] + bv));
+                v.y = pack2(from_f32<T>(acc[mb][nb][4 * q + 2] + bv), from_f32<T>(acc[mb][nb][4 * q + 3] + bv));
+                *reinterpret_cast<uint2*>(scr + li * 32 + 8 * q + 4 * g) = v;
+              }
+            }
+            // A wave's LDS operations execute in order, so only the compiler
+            // must be kept from reordering the scratch writes and reads.
+            __builtin_amdgcn_wave_barrier();
+            if (MODE != MODE_T2FWD && pos_contig) {
+              // 8 consecutive positions of one channel per lane (NCDHW).
+#pragma unroll
+              for (int rd2 = 0; rd2 < 2; ++rd2) {
+                const int id = rd2 * 64 + lane;
+                const int c = id >> 2, pc = id & 3;
+                const int col = colbase + c;
+                const int rw = r0w + pc * 8;
+                const uint4 v = *reinterpret_cast<const uint4*>(scr + c * 32 + pc * 8);
+                if (col < a.ncols && rw < a.Rw) {
+                  uint16_t* p = dstn + (int64_t)col * sd[1] + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + rw;
+                  if (rw + 8 <= a.Rw && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+                    *reinterpret_cast<uint4*>(p) = v;
+                  } else {
+                    for (int k = 0; k < 8 && rw + k < a.Rw; ++k) p[k] = u4_elem(v, k);
+                  }
+                }
+              }
+            } else if (ch_contig && (MODE != MODE_T2FWD || a.cout_t2 % 8 == 0)) {
+              // 8 consecutive channels of one position per lane (NDHWC).
+              const int sl = lane & 15;
+#pragma unroll
+              for (int rd2 = 0; rd2 < 2; ++rd2) {
+                const int task = rd2 * 4 + (lane >> 4);
+                const int p0 = 16 * (task & 1), c0 = 8 * (task >> 1);
+                const int a0 = (c0 + (sl >> 2)) * 32 + p0 + 4 * (sl & 3);
+                const uint4 v = lds_tr_pair(scr, a0, a0 + 4 * 32);
+                const int col = colbase + c0;
+                const int rw = r0w + p0 + sl;
+                if (col < a.ncols && rw < a.Rw) {
+                  uint16_t* p;
+                  int nvalid;
+                  if (MODE == MODE_T2FWD) {
+                    const int tap = col / a.cout_t2, co = col - tap * a.cout_t2;
+                    const int kd = tap >> 2, kh = (tap >> 1) & 1, kw = tap & 1;
+                    p = dstn + (int64_t)co + (int64_t)(2 * rd + kd) * sd[2] + (int64_t)(2 * rh + kh) * sd[3] +
+                        (int64_t)(2 * rw + kw) * sd[4];
+                    nvalid = 8;
+                  } else {
+                    p = dstn + (int64_t)col + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + (int64_t)rw * sd[4];
+                    nvalid = a.ncols - col < 8 ? a.ncols - col : 8;
+                  }
+                  if (nvalid == 8 && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+                    *reinterpret_cast<uint4*>(p) = v;
+                  } else {
+                    for (int k = 0; k < nvalid; ++k) p[k] = u4_elem(v, k);
+                  }
+                }
+              }
+            } else {
+              // Any other strides: one element per lane from the scratch.
+              for (int e = lane; e < 32 * 32; e += 64) {
+                const int c = e >> 5, pp = e & 31;
+                const int col = colbase + c;
+                const int rw = r0w + pp;
+                if (col >= a.ncols || rw >= a.Rw) continue;
+                const uint16_t v = scr[c * 32 + pp];
+                if (MODE == MODE_T2FWD) {
+                  const int tap = col / a.cout_t2, co = col - tap * a.cout_t2;
+                  const int kd = tap >> 2, kh = (tap >> 1) & 1, kw = tap & 1;
+                  dstn[(int64_t)co * sd[1] + (int64_t)(2 * rd + kd) * sd[2] + (int64_t)(2 * rh + kh) * sd[3] +
+                       (int64_t)(2 * rw + kw) * sd[4]] = v;
+                } else {
+                  dstn[(int64_t)col * sd[1] + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + (int64_t)rw * sd[4]] = v;
+                }
+              }
+            }
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
+      }
+    }
+    if (!more) break;
+    job = njob;
+    chunk = nchunk;
+    ++t;
+  }
+}
+
+template <typename T, int MODE, int NB, int CL, int WF>
+static void launch_row_inst(const RowArgs& a, int grid, size_t lds, hipStream_t stream) {
+  auto kern = row_kernel<T, MODE, NB, CL, WF>;
+  if (lds > 65536) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, a);
+}
+
+}  // namespace r3c

@@ -1,22 +1,69 @@
-// r3c_wgrad_k3.hip -- instantiations of the weight-gradient kernel for 3x3x3 Conv3d.
-#include "r3c_igemm_wgrad.h"
+// r3c_wgrad_k3.hip -- instantiations of the weight-gradient kernel, mode MODE_K3.
+#include "r3c_wgrad.h"
 
 namespace r3c {
 
-bool launch_wgrad_k3(int dtype, int fb, int cbw, const WgradArgs& a, size_t lds, hipStream_t s) {
-#define R3C_CASE(T, FB, CBW)                               \
-  if (fb == FB && cbw == CBW) {                            \
-    launch_wgrad_inst<T, MODE_K3, FB, CBW>(a, lds, s);     \
-    return true;                                           \
+bool launch_wgrad_k3_bf16(int cbw, const WgArgs& a, size_t lds, hipStream_t s) {
+  if (cbw == 1) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 1>(a, lds, s);
+    return true;
   }
-#define R3C_CASES(T) R3C_CASE(T, 1, 7) R3C_CASE(T, 1, 14) R3C_CASE(T, 2, 7) R3C_CASE(T, 2, 14) R3C_CASE(T, 3, 7)
-  if (dtype == DT_BF16) {
-    R3C_CASES(bf16_tag)
-  } else {
-    R3C_CASES(f16_tag)
+  if (cbw == 2) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 2>(a, lds, s);
+    return true;
   }
-#undef R3C_CASES
-#undef R3C_CASE
+  if (cbw == 3) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 3>(a, lds, s);
+    return true;
+  }
+  if (cbw == 4) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 4>(a, lds, s);
+    return true;
+  }
+  if (cbw == 5) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 5>(a, lds, s);
+    return true;
+  }
+  if (cbw == 6) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 6>(a, lds, s);
+    return true;
+  }
+  if (cbw == 7) {
+    launch_wgrad_inst<bf16_tag, MODE_K3, 7>(a, lds, s);
+    return true;
+  }
+  return false;
+}
+
+bool launch_wgrad_k3_f16(int cbw, const WgArgs& a, size_t lds, hipStream_t s) {
+  if (cbw == 1) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 2) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 2>(a, lds, s);
+    return true;
+  }
+  if (cbw == 3) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 3>(a, lds, s);
+    return true;
+  }
+  if (cbw == 4) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 4>(a, lds, s);
+    return true;
+  }
+  if (cbw == 5) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 5>(a, lds, s);
+    return true;
+  }
+  if (cbw == 6) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 6>(a, lds, s);
+    return true;
+  }
+  if (cbw == 7) {
+    launch_wgrad_inst<f16_tag, MODE_K3, 7>(a, lds, s);
+    return true;
+  }
   return false;
 }
 
