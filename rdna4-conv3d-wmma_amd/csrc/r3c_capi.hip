@@ -19,8 +19,8 @@
 namespace r3c {
 
 #define R3C_DECL_ROW(m)                                                                       \
-  bool launch_row_##m##_bf16(int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s); \
-  bool launch_row_##m##_f16(int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s);
+  bool launch_row_##m##_bf16(int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s); \
+  bool launch_row_##m##_f16(int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s);
 R3C_DECL_ROW(k3)
 R3C_DECL_ROW(k1)
 R3C_DECL_ROW(t2dx)
@@ -34,18 +34,18 @@ R3C_DECL_WG(k1)
 R3C_DECL_WG(t2dw)
 #undef R3C_DECL_WG
 
-bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds, hipStream_t s) {
+bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s) {
   const bool bf = dtype == R3C_BF16;
   switch (mode) {
     case MODE_K3:
-      return bf ? launch_row_k3_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_k3_f16(nb, cl, wf, a, grid, lds, s);
+      return bf ? launch_row_k3_bf16(nb, cl, wf, a, cus, lds, s) : launch_row_k3_f16(nb, cl, wf, a, cus, lds, s);
     case MODE_K1:
-      return bf ? launch_row_k1_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_k1_f16(nb, cl, wf, a, grid, lds, s);
+      return bf ? launch_row_k1_bf16(nb, cl, wf, a, cus, lds, s) : launch_row_k1_f16(nb, cl, wf, a, cus, lds, s);
     case MODE_T2DX:
-      return bf ? launch_row_t2dx_bf16(nb, cl, wf, a, grid, lds, s) : launch_row_t2dx_f16(nb, cl, wf, a, grid, lds, s);
+      return bf ? launch_row_t2dx_bf16(nb, cl, wf, a, cus, lds, s) : launch_row_t2dx_f16(nb, cl, wf, a, cus, lds, s);
     case MODE_T2FWD:
-      return bf ? launch_row_t2fwd_bf16(nb, cl, wf, a, grid, lds, s)
-                : launch_row_t2fwd_f16(nb, cl, wf, a, grid, lds, s);
+      return bf ? launch_row_t2fwd_bf16(nb, cl, wf, a, cus, lds, s)
+                : launch_row_t2fwd_f16(nb, cl, wf, a, cus, lds, s);
     default: return false;
   }
 }
@@ -191,10 +191,17 @@ int validate(const r3c_conv_desc* d, bool transpose) {
   return check_strides(d->y_strides, yd, "y");
 }
 
+// Compute units of the current device (set by check_device, per thread).
+thread_local int t_cus = kNumCUs;
+
 int check_device() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(R3C_HIP_ERROR, "hipGetDevice failed");
   if (!r3c_device_supported(dev)) return fail(R3C_UNSUPPORTED, "device %d is not gfx950", dev);
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = kNumCUs;
+  t_cus = cus;
   return R3C_OK;
 }
 
@@ -333,13 +340,34 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
     a.HD = a.TD; a.HH = a.TH; hw = 32;
   }
   const int hpos = a.HD * a.HH * hw;
-  a.CGS = (hpos + 255) / 256 * 256;
+  a.CGS = (hpos + 15) / 16 * 16;  // 256-byte aligned channel-group planes
   const int taps = taps_k;
   const int nstep = cdiv(taps * g8, 2);
   const int64_t wchunk = (int64_t)nstep * p.nb * 1024;  // bytes of one chunk's fragments
-  a.wfull = (a.n_ctiles == 1 && wchunk * a.nchunks <= 48 * 1024) ? 1 : 0;
-  const int64_t wbytes = a.wfull ? wchunk * a.nchunks : 2 * wchunk;
-  p.lds = (size_t)(2 * g8 * a.CGS * 16 + wbytes + 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4 + (int64_t)nstep * 2 * 4);
+  // Buffering options in order of preference; take the first that leaves room
+  // for two workgroups per CU (8 waves), else the one with the most room.
+  //   wfull: every chunk's weights resident (only with a single column tile)
+  //   nbuf 2: double-buffered stages, one barrier per stage; 1: two barriers
+  const int64_t fixed = 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4 + (int64_t)nstep * 2 * 4;
+  const int64_t act1 = (int64_t)g8 * a.CGS * 16;
+  struct Opt { int wfull, nbuf; };
+  static const Opt opts2[] = {{1, 2}, {0, 2}, {1, 1}, {0, 1}};
+  int best = -1;
+  int64_t best_lds = 0;
+  for (const Opt& o : opts2) {
+    if (o.wfull && a.n_ctiles != 1) continue;
+    const int64_t l = fixed + o.nbuf * act1 + (o.wfull ? wchunk * a.nchunks : o.nbuf * wchunk);
+    if (l > kMaxLds) continue;
+    if (best < 0 || kMaxLds / l > kMaxLds / best_lds) {
+      best = (int)(&o - opts2);
+      best_lds = l;
+    }
+    if (kMaxLds / l >= 2) break;
+  }
+  if (best < 0) best = 3, best_lds = fixed + act1 + wchunk;  // rejected by the LDS check
+  a.wfull = opts2[best].wfull;
+  a.nbuf = opts2[best].nbuf;
+  p.lds = (size_t)best_lds;
   PackArgs& pk = p.pk;
   memset(&pk, 0, sizeof pk);
   pk.cs = cs;
@@ -389,10 +417,10 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   const int64_t jobs = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
   if (jobs >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
   a.njobs = (int32_t)jobs;
-  const int per_cu = (int)std::max<int64_t>(1, std::min<int64_t>(4, kMaxLds / (int64_t)std::max<size_t>(p.lds, 1)));
-  const int grid = (int)std::min<int64_t>(jobs, (int64_t)kNumCUs * per_cu);
+  // The launcher sizes the grid to the resident capacity (CUs x workgroups
+  // per CU from the occupancy query); workgroups take contiguous job ranges.
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = launch_row(d->dtype, p.mode, p.nb, p.cl, a.wfull, a, grid, p.lds, s);
+  const bool launched = launch_row(d->dtype, p.mode, p.nb, p.cl, a.wfull, a, t_cus, p.lds, s);
   tl.end();
   if (!launched)
     return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d cl %d", p.mode, p.ck, p.nb,

@@ -42,8 +42,9 @@ struct RowArgs {
   int32_t ncols;           // real columns (Cd, or 8 * Cout for T2FWD)
   int32_t cout_t2;         // T2FWD: Cout, to split a column into (tap, channel)
   int32_t HD, HH;          // LDS tile dims (the w extent is fixed per mode)
-  int32_t CGS;             // 16-byte slots per activation buffer (HD*HH*HW rounded up to 256)
+  int32_t CGS;             // 16-byte slots per channel-group plane (HD*HH*HW rounded up to 16)
   int32_t wfull;           // 1: every chunk's weights stay resident in LDS
+  int32_t nbuf;            // 2: double-buffered stages; 1: single buffers, two barriers per stage
   int32_t src_cl;          // 1: channel-contiguous 16-byte source loads are legal
   int32_t njobs;           // (box, column tile) jobs; workgroups stride over them
 };
@@ -95,7 +96,8 @@ struct PackArgs {
 };
 
 // Host launchers (return false when no instantiation matches).
-bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int grid, size_t lds_bytes,
+// `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
+bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
                 hipStream_t stream);
 bool launch_wgrad(int dtype, int mode, int cbw, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);

@@ -85,7 +85,7 @@ __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
 }
 
 // LDS: act[2][G8][HPAD] 16-byte slots (double-buffered tile, HPAD = HPOS rounded
-// up to 256), the weight fragments (all of K when WF, else two chunk buffers of
+// up to 16), the weight fragments (all of K when WF, else two chunk buffers of
 // NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB), the bias
 // table (fp32, one per packed column) and the tap table.
 //
@@ -104,7 +104,7 @@ __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
 // ds_read_tr16_b64, 8 consecutive channels of one position per lane when
 // channels are contiguous (NDHWC) -- so every global store is 16 bytes.
 template <typename T, int MODE, int NB, int CL, int WF>
-__global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void row_kernel(const RowArgs a) {
   extern __shared__ uint4 smem4[];
   constexpr int TAPS = RowGeom<MODE>::TAPS;
   constexpr int HW = RowGeom<MODE>::HW;
@@ -123,11 +123,12 @@ __global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
 
   const int HH = a.HH;
   const int HPOS = a.HD * HH * HW;
-  const int HPAD = a.CGS;  // HPOS rounded up to a multiple of 256
+  const int HPAD = a.CGS;  // HPOS rounded up to a multiple of 16
   const int ABUF = G8 * HPAD;  // slots per activation buffer
+  const int nbuf = a.nbuf;     // 2: double-buffered stages; 1: single buffers, two barriers
   uint4* act = smem4;
-  uint4* wts = smem4 + 2 * ABUF;
-  const int wslots = WF ? a.nchunks * WFRAG : 2 * WFRAG;
+  uint4* wts = smem4 + nbuf * ABUF;
+  const int wslots = WF ? a.nchunks * WFRAG : nbuf * WFRAG;
   uint16_t* scr = reinterpret_cast<uint16_t*>(wts + wslots) + wv * 1024;
   float* btab = reinterpret_cast<float*>(wts + wslots + 4 * 128);
   const int nbcol = a.nbt_pad * 32;
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
     for (int cg = 0; cg < G8; ++cg)
 #pragma unroll
       for (int k = 0; k < MAXK; ++k)
-        if (k * 256 < HPAD) act[buf * ABUF + cg * HPAD + k * 256 + tid] = pfa[cg * MAXK + k];
+        if (k * 256 + tid < HPOS) act[buf * ABUF + cg * HPAD + k * 256 + tid] = pfa[cg * MAXK + k];
     if (!WF) {
 #pragma unroll
       for (int i = 0; i < WIT; ++i) {
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
   int job = j0, chunk = 0, t = 0;
   issue(job, 0);
   while (true) {
-    const int buf = t & 1;
+    const int buf = nbuf == 2 ? (t & 1) : 0;
     commit(buf);
     __syncthreads();
     int njob = job, nchunk = chunk + 1;
@@ -422,6 +423,7 @@ __global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
       }
     }
     if (!more) break;
+    if (nbuf == 1) __syncthreads();  // every wave is done with the buffers the next commit overwrites
     job = njob;
     chunk = nchunk;
     ++t;
@@ -429,9 +431,13 @@ __global__ __launch_bounds__(256) void row_kernel(const RowArgs a) {
 }
 
 template <typename T, int MODE, int NB, int CL, int WF>
-static void launch_row_inst(const RowArgs& a, int grid, size_t lds, hipStream_t stream) {
+static void launch_row_inst(const RowArgs& a, int cus, size_t lds, hipStream_t stream) {
   auto kern = row_kernel<T, MODE, NB, CL, WF>;
   if (lds > 65536) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 256, lds) != hipSuccess || occ < 1) occ = 1;
+  const int64_t cap = (int64_t)cus * occ;
+  const int grid = (int)(a.njobs < cap ? a.njobs : cap);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, a);
 }
 
