@@ -68,20 +68,10 @@ __device__ __forceinline__ void store_elem(void* base, int64_t i, int dtype, flo
   else reinterpret_cast<uint16_t*>(base)[i] = from_f32<f16_tag>(v);
 }
 
-// One block = 64 output elements x 4 split quarters.  Quarter q adds splits
-// [q*S/4, (q+1)*S/4) in increasing order; the four quarter sums are then added
-// in the order 0, 1, 2, 3.  The result is bitwise reproducible run to run.
-// Elements [0, Fc*taps*Gc) are dW (walked with G fastest, matching the partial
-// layout for coalesced reads); the tail holds db.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const ReduceArgs a) {
-  __shared__ float red[4][64];
-  const int lane = threadIdx.x & 63;
-  const int q = threadIdx.x >> 6;
-  const int64_t nw = (int64_t)a.Fc * a.taps * a.Gc;
-  const int ndb = a.db_mode == 1 ? a.Fc : (a.db_mode == 2 ? a.Gc : 0);
-  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
-  const int s0 = (int)(((int64_t)q * a.nsplit) / 4);
-  const int s1 = (int)(((int64_t)(q + 1) * a.nsplit) / 4);
+// Element e of the reduce: [0, Fc*taps*Gc) are dW, walked with G fastest
+// (matching the partial layout, so a wave reads consecutive floats); the tail
+// holds db.  split_sum adds splits [s0, s1) of one element in increasing order.
+__device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64_t nw, int s0, int s1) {
   float sum = 0.f;
   if (e < nw) {
     const int gch = (int)(e % a.Gc);
@@ -90,10 +80,12 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const ReduceArgs a) {
     const int f = (int)(r / a.taps);
     const size_t stride = (size_t)a.Fpad * a.taps * a.Gpad;
     const float* p = a.part + ((size_t)f * a.taps + tap) * a.Gpad + gch;
+#pragma unroll 8
     for (int s = s0; s < s1; ++s) sum += p[(size_t)s * stride];
-  } else if (e < nw + ndb) {
+  } else {
     const int c = (int)(e - nw);
     if (a.db_mode == 1) {
+#pragma unroll 8
       for (int s = s0; s < s1; ++s) sum += a.dbpart[(size_t)s * a.Fpad + c];
     } else {
       for (int s = s0; s < s1; ++s) {
@@ -103,27 +95,50 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const ReduceArgs a) {
       }
     }
   }
-  red[q][lane] = sum;
-  __syncthreads();
-  if (q == 0) {
-    const float tot = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-    if (e < nw) {
-      const int gch = (int)(e % a.Gc);
-      const int64_t r = e / a.Gc;
-      const int tap = (int)(r % a.taps);
-      const int f = (int)(r / a.taps);
-      store_elem<float>(a.dw, ((int64_t)f * a.Gc + gch) * a.taps + tap, a.dw_dtype, tot);
-    } else if (e < nw + ndb) {
-      store_elem<float>(a.db, e - nw, a.db_dtype, tot);
-    }
+  return sum;
+}
+
+// First level: group blockIdx.y sums splits [y*kReduceGroup, (y+1)*kReduceGroup).
+__global__ __launch_bounds__(256) void wgrad_reduce_groups_kernel(const ReduceArgs a, int64_t nw, int64_t ne) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= ne) return;
+  const int s0 = blockIdx.y * kReduceGroup;
+  const int s1 = s0 + kReduceGroup < a.nsplit ? s0 + kReduceGroup : a.nsplit;
+  a.lvl2[(size_t)blockIdx.y * ne + e] = split_sum(a, e, nw, s0, s1);
+}
+
+// Last level: the group sums in increasing group order (or, with one group,
+// the splits themselves), converted to the output dtype.  Bitwise
+// reproducible run to run: every sum has a fixed order.
+__global__ __launch_bounds__(256) void wgrad_reduce_final_kernel(const ReduceArgs a, int64_t nw, int64_t ne) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= ne) return;
+  float tot;
+  if (a.ngroups <= 1) {
+    tot = split_sum(a, e, nw, 0, a.nsplit);
+  } else {
+    tot = 0.f;
+    for (int gi = 0; gi < a.ngroups; ++gi) tot += a.lvl2[(size_t)gi * ne + e];
+  }
+  if (e < nw) {
+    const int gch = (int)(e % a.Gc);
+    const int64_t r = e / a.Gc;
+    const int tap = (int)(r % a.taps);
+    const int f = (int)(r / a.taps);
+    store_elem<float>(a.dw, ((int64_t)f * a.Gc + gch) * a.taps + tap, a.dw_dtype, tot);
+  } else {
+    store_elem<float>(a.db, e - nw, a.db_dtype, tot);
   }
 }
 
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream) {
   const int64_t nw = (int64_t)a.Fc * a.taps * a.Gc;
   const int ndb = a.db_mode == 1 ? a.Fc : (a.db_mode == 2 ? a.Gc : 0);
-  const int64_t blocks = (nw + ndb + 63) / 64;
-  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  const int64_t ne = nw + ndb;
+  const unsigned blocks = (unsigned)((ne + 255) / 256);
+  if (a.ngroups > 1)
+    hipLaunchKernelGGL(wgrad_reduce_groups_kernel, dim3(blocks, (unsigned)a.ngroups), dim3(256), 0, stream, a, nw, ne);
+  hipLaunchKernelGGL(wgrad_reduce_final_kernel, dim3(blocks), dim3(256), 0, stream, a, nw, ne);
 }
 
 }  // namespace r3c

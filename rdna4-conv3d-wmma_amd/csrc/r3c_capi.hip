@@ -27,8 +27,8 @@ R3C_DECL_ROW(t2dx)
 R3C_DECL_ROW(t2fwd)
 #undef R3C_DECL_ROW
 #define R3C_DECL_WG(m)                                                                    \
-  bool launch_wgrad_##m##_bf16(int cbw, const WgArgs& a, size_t lds, hipStream_t s); \
-  bool launch_wgrad_##m##_f16(int cbw, const WgArgs& a, size_t lds, hipStream_t s);
+  bool launch_wgrad_##m##_bf16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s); \
+  bool launch_wgrad_##m##_f16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s);
 R3C_DECL_WG(k3)
 R3C_DECL_WG(k1)
 R3C_DECL_WG(t2dw)
@@ -50,12 +50,12 @@ bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, i
   }
 }
 
-bool launch_wgrad(int dtype, int mode, int cbw, const WgArgs& a, size_t lds, hipStream_t s) {
+bool launch_wgrad(int dtype, int mode, int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s) {
   const bool bf = dtype == R3C_BF16;
   switch (mode) {
-    case MODE_K3: return bf ? launch_wgrad_k3_bf16(cbw, a, lds, s) : launch_wgrad_k3_f16(cbw, a, lds, s);
-    case MODE_K1: return bf ? launch_wgrad_k1_bf16(cbw, a, lds, s) : launch_wgrad_k1_f16(cbw, a, lds, s);
-    case MODE_T2DW: return bf ? launch_wgrad_t2dw_bf16(cbw, a, lds, s) : launch_wgrad_t2dw_f16(cbw, a, lds, s);
+    case MODE_K3: return bf ? launch_wgrad_k3_bf16(cbw, cl, a, lds, s) : launch_wgrad_k3_f16(cbw, cl, a, lds, s);
+    case MODE_K1: return bf ? launch_wgrad_k1_bf16(cbw, cl, a, lds, s) : launch_wgrad_k1_f16(cbw, cl, a, lds, s);
+    case MODE_T2DW: return bf ? launch_wgrad_t2dw_bf16(cbw, cl, a, lds, s) : launch_wgrad_t2dw_f16(cbw, cl, a, lds, s);
     default: return false;
   }
 }
@@ -139,7 +139,6 @@ struct TimedLaunch {
 };
 
 constexpr int64_t kMaxLds = 160 * 1024;
-constexpr int kWgTarget = 512;                 // weight-gradient workgroups to aim for
 constexpr int kNumCUs = 256;                   // MI355X compute units
 constexpr int64_t kMaxPartialBytes = 96ll << 20;
 
@@ -432,10 +431,10 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // Weight-gradient plan (Conv3d dW k1/k3, ConvTranspose dW)
 // ---------------------------------------------------------------------------
 struct WgPlan {
-  int mode, cbw, taps;
+  int mode, cbw, taps, ngroups;
   WgArgs a;
   size_t lds;
-  int64_t part_bytes, dbpart_bytes;
+  int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
 };
 
 void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
@@ -470,40 +469,37 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   a.n_gtiles = cdiv(a.Gc, a.GCW);
   a.Fpad = a.n_ftiles * 32;
   a.Gpad = a.n_gtiles * a.GCW;
-  const int ncb = cdiv((int64_t)p.taps * (a.GCW / 4), 8);
-  p.cbw = cdiv(ncb, 4);
-  const int cbw_max = p.mode == MODE_K3 ? 7 : (p.mode == MODE_K1 ? 2 : 4);
+  const int ncb = cdiv((int64_t)p.taps * (a.GCW / 4), 8);  // 32-column blocks
+  p.cbw = cdiv(ncb, 8);                                      // per wave, 8 waves
+  const int cbw_max = p.mode == MODE_K3 ? 4 : (p.mode == MODE_K1 ? 1 : 2);
   if (p.cbw > cbw_max) p.cbw = cbw_max;  // cannot happen with GCW <= 32
-  // Box: TD x TH x 16 positions.
-  if (p.mode == MODE_K3) {
-    a.TD = 2; a.TH = 4;
-    if ((int64_t)256 * 32 * 2 + (int64_t)6 * 6 * 18 * a.GCW * 2 <= 50 * 1024) { a.TD = 4; a.TH = 4; }
-    a.HD = a.TD + 2; a.HH = a.TH + 2; a.HW = 18;
-  } else if (p.mode == MODE_K1) {
-    a.TD = 4; a.TH = 4;
-    a.HD = a.TD; a.HH = a.TH; a.HW = 16;
-  } else {
-    a.TD = 2; a.TH = 2;
-    a.HD = 2 * a.TD; a.HH = 2 * a.TH; a.HW = 32;
-  }
-  a.th_log2 = a.TH == 1 ? 0 : (a.TH == 2 ? 1 : (a.TH == 4 ? 2 : 3));
-  a.nbd = cdiv(a.Rd, a.TD);
-  a.nbh = cdiv(a.Rh, a.TH);
+  // Box geometry is fixed per mode (WgGeom).
+  int TD, TH, lds;
+  if (p.mode == MODE_K3) TD = WgGeom<MODE_K3>::TD, TH = WgGeom<MODE_K3>::TH, lds = WgGeom<MODE_K3>::LDS_BYTES;
+  else if (p.mode == MODE_K1) TD = WgGeom<MODE_K1>::TD, TH = WgGeom<MODE_K1>::TH, lds = WgGeom<MODE_K1>::LDS_BYTES;
+  else TD = WgGeom<MODE_T2DW>::TD, TH = WgGeom<MODE_T2DW>::TH, lds = WgGeom<MODE_T2DW>::LDS_BYTES;
+  a.nbd = cdiv(a.Rd, TD);
+  a.nbh = cdiv(a.Rh, TH);
   a.nbw = cdiv(a.Rw, 16);
   const int64_t nbox = (int64_t)d->n * a.nbd * a.nbh * a.nbw;
   a.nbox = (int32_t)std::min<int64_t>(nbox, (1ll << 31) - 1);
   const int tiles = a.n_ftiles * a.n_gtiles;
   const int64_t per_split = (int64_t)a.Fpad * p.taps * a.Gpad * 4;
-  int64_t nsplit = cdiv(kWgTarget, tiles);
+  // Enough workgroups to fill every CU at the LDS-limited occupancy, no more:
+  // each extra split costs partial traffic.
+  const int64_t wg_target = (int64_t)kNumCUs * std::max<int64_t>(1, kMaxLds / lds);
+  int64_t nsplit = cdiv(wg_target, tiles);
   nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, nbox));
   a.nsplit = (int32_t)nsplit;
   a.nblocks = (int32_t)(nsplit * tiles);
-  const int64_t boxpos = (int64_t)a.TD * a.TH * 16;
-  const int64_t hpos = (int64_t)a.HD * a.HH * a.HW;
-  p.lds = (size_t)(boxpos * 32 * 2 + hpos * a.GCW * 2);
+  p.lds = (size_t)lds;
   p.part_bytes = align256(nsplit * per_split);
   p.dbpart_bytes = align256(nsplit * (int64_t)std::max(a.Fpad, p.taps * a.Gpad) * 4);
+  // Two-level reduce: group sums of kReduceGroup splits, then their sum.
+  p.ngroups = cdiv(nsplit, kReduceGroup);
+  p.nelem = (int64_t)a.Fc * p.taps * a.Gc + std::max(a.Fc, a.Gc);
+  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
 }
 
 int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void* dy, void* dw, int dw_dtype, void* db,
@@ -513,9 +509,9 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
   if (p.a.f_bytes == 0 || p.a.g_bytes == 0)
     return fail(R3C_UNSUPPORTED, "one sample exceeds 1 GiB (32-bit buffer offsets)");
-  if (ws_bytes < p.part_bytes + p.dbpart_bytes)
-    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes,
-                (long long)(p.part_bytes + p.dbpart_bytes));
+  const int64_t need = p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
+  if (ws_bytes < need)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
   if (dw_dtype != R3C_F32 && dw_dtype != d->dtype) return fail(R3C_INVALID, "dw_dtype must be fp32 or the input dtype");
   if (db && db_dtype != R3C_F32 && db_dtype != R3C_F16 && db_dtype != R3C_BF16)
@@ -528,11 +524,11 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
-  a.f_cl = (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0) ? 1 : 0;
-  a.g_cl = (vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0) ? 1 : 0;
+  // Channel-contiguous 16-byte staging when both operands allow it, else 8 scalar loads per slot.
+  const int cl = (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0 && vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0) ? 1 : 0;
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
   TimedLaunch tl(KIND_WGRAD, s);
-  const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, a, p.lds, s);
+  const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, a, p.lds, s);
   tl.end();
   if (!launched) return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d cbw %d", p.mode, p.cbw);
   rc = check_launch("weight-gradient kernel");
@@ -552,6 +548,8 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   r.dw_dtype = dw_dtype;
   r.db_dtype = db_dtype;
   r.db_mode = a.db_mode;
+  r.ngroups = p.ngroups;
+  r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
   {
     TimedLaunch tr(KIND_REDUCE, s);
     launch_wgrad_reduce(r, s);
@@ -571,7 +569,7 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   WgPlan p;
   plan_wgrad(d, transpose, p);
-  return p.part_bytes + p.dbpart_bytes;
+  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
 }
 
 std::mutex g_dev_mu;

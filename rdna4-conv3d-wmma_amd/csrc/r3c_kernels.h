@@ -49,6 +49,26 @@ struct RowArgs {
   int32_t njobs;           // (box, column tile) jobs; workgroups stride over them
 };
 
+// Weight-gradient box geometry, fixed per mode: TD x TH lines of 16
+// positions along w (the K block of one staging round), and the G tile = the
+// box plus its tap halo.  Both LDS tiles are [position][32 channels].
+template <int MODE>
+struct WgGeom {
+  static constexpr int TAPS = MODE == MODE_K3 ? 27 : (MODE == MODE_T2DW ? 8 : 1);
+  static constexpr int TD = MODE == MODE_T2DW ? 2 : 4;
+  static constexpr int TH = MODE == MODE_T2DW ? 2 : 4;
+  static constexpr int HD = MODE == MODE_K3 ? TD + 2 : (MODE == MODE_T2DW ? 2 * TD : TD);
+  static constexpr int HH = MODE == MODE_K3 ? TH + 2 : (MODE == MODE_T2DW ? 2 * TH : TH);
+  static constexpr int HW = MODE == MODE_K3 ? 18 : (MODE == MODE_T2DW ? 32 : 16);
+  static constexpr int LINES = TD * TH;
+  static constexpr int BOXPOS = LINES * 16;
+  static constexpr int HPOS = HD * HH * HW;
+  static constexpr int THREADS = 512;                                 // 8 waves
+  static constexpr int NFI = (BOXPOS * 4 + THREADS - 1) / THREADS;   // F staging items (8 channels) per thread
+  static constexpr int NGI = (HPOS * 4 + THREADS - 1) / THREADS;     // G staging items per thread at GCW = 32
+  static constexpr int LDS_BYTES = 2 * (BOXPOS + HPOS) * 64;          // double-buffered tiles
+};
+
 struct WgArgs {
   const uint16_t* fsrc;  // F operand tensor (dY for Conv3d, x for ConvTranspose)
   const uint16_t* gsrc;  // G operand tensor (x for Conv3d, dY for ConvTranspose)
@@ -60,14 +80,11 @@ struct WgArgs {
   int32_t Rd, Rh, Rw;      // F (row) grid
   int32_t Gd, Gh, Gw;      // G grid
   int32_t pd, ph, pw;      // Conv3d padding
-  int32_t TD, TH, th_log2; // box = TD x TH x 16 positions; TH is a power of two
-  int32_t nbd, nbh, nbw, nbox;
+  int32_t nbd, nbh, nbw, nbox;  // boxes (WgGeom) per dimension and in total
   int32_t nsplit;
   int32_t n_ftiles, n_gtiles;
-  int32_t GCW;             // G channels per tile (multiple of 8)
+  int32_t GCW;             // G channels per tile (multiple of 8, at most 32)
   int32_t Fpad, Gpad;
-  int32_t HD, HH, HW;      // G tile dims
-  int32_t f_cl, g_cl;      // channel-contiguous 16-byte loads legal
   int32_t db_mode;         // 0 none, 1 db = sum over F, 2 db = sum over G
   int32_t nblocks;
 };
@@ -75,12 +92,16 @@ struct WgArgs {
 struct ReduceArgs {
   const float* part;
   const float* dbpart;
+  float* lvl2;            // [ngroups][nelem] group sums (two-level reduce only)
   void* dw;
   void* db;
   int32_t nsplit, Fc, Gc, taps, Fpad, Gpad;
   int32_t dw_dtype, db_dtype;
   int32_t db_mode;        // 0 none, 1 from F partials, 2 from G partials
+  int32_t ngroups;        // split groups of kReduceGroup; 1 = single pass straight to dW / db
 };
+
+constexpr int kReduceGroup = 32;  // splits summed per thread in the first reduce level
 
 struct PackArgs {
   const uint16_t* w;
@@ -99,8 +120,9 @@ struct PackArgs {
 // `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
                 hipStream_t stream);
-bool launch_wgrad(int dtype, int mode, int cbw, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
+bool launch_wgrad(int dtype, int mode, int cbw, int cl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
+// One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 
 }  // namespace r3c

@@ -7,41 +7,55 @@
 //   ConvTranspose dW (T2DW): F = x (row grid = input grid), G = dY at 2p + tap,
 //                        dW[ci = f][co = g][tap]     (conv3d_wmma.py:934-1012)
 //
-// A workgroup owns one 32-channel F block (MFMA rows), one G channel range of
-// GCW channels, all taps, and a fixed contiguous range of TD x TH x 16
+// A workgroup (8 waves) owns one 32-channel F block (MFMA rows), one G channel
+// range of GCW <= 32 channels, all taps, and a fixed contiguous range of
 // position boxes (its split of K; deterministic).  The MFMA columns are the
 // (tap, 4-channel quad) pairs of the range, flattened and cut into blocks of 32
-// columns, so a 24-channel layer wastes no columns on channel padding; each
-// wave owns CBW column blocks.
+// columns, so a 24-channel layer wastes no columns on channel padding; wave w
+// owns column blocks w, w+8, w+16, ... (CBW of them at most).  The last wave,
+// which has the fewest blocks, also accumulates the F-side bias gradient.
 //
-// Both operands need k to run over positions while lanes run over channels.
-// The tiles are [position][channel] in LDS and the operands come from
-// ds_read_tr16_b64 (inside a 16-lane group: out[4a + b][i] = lds16[addr[a + 4i] + b]):
-// source lane s supplies the address of position 8g + s/4 (+4 for the second
-// read) and of channel quad s%4 of its group, so every group of four output
-// lanes may take its quad from a different tap -- that is what lets columns
-// mix taps.  A tap only moves the row address, so alignment always holds.
+// Box geometry is fixed per mode: TD x TH lines of 16 positions along w, and
+// the G tile is the box plus its tap halo.  Both LDS tiles are
+// [position][32 channels] (64-byte rows), so every LDS offset the K loop uses
+// is a compile-time immediate.
+//
+// Both MFMA operands need k to run over positions while lanes run over
+// channels; they come from ds_read_tr16_b64 (inside a 16-lane group:
+// out[4a + b][i] = lds16[addr[a + 4i] + b]).  Source lane s supplies the
+// address of position 8g + s/4 (+4 for the second read) and of channel quad
+// s%4 of its group, so every group of four output lanes may take its quad from
+// a different tap -- that is what lets columns mix taps.  A tap only moves the
+// row address, so alignment always holds.
+//
+// Pipeline: double-buffered LDS tiles, one barrier per box.  After the barrier
+// the registers holding box b+1 are written to the free buffer, the loads of
+// box b+2 are issued into those registers, and box b is computed.
 //
 // The bias gradient is one extra MFMA per step against an all-ones operand:
 // db = sum F (db_mode 1, Conv3d) or sum G (db_mode 2, ConvTranspose, summed
-// over taps by the reduce kernel).  Each split writes fp32 partials
-// [split][Fpad][TAPS][Gpad]; wgrad_reduce_kernel adds the splits in a fixed
+// over taps by the reduce).  Each split writes fp32 partials
+// [split][Fpad][TAPS][Gpad]; the reduce kernels add the splits in a fixed
 // order.
 #pragma once
 #include "r3c_row.h"
 
 namespace r3c {
 
-template <int MODE>
-struct WgGeom {
-  static constexpr int TAPS = MODE == MODE_K3 ? 27 : (MODE == MODE_T2DW ? 8 : 1);
-};
 
-template <typename T, int MODE, int CBW>
-__global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
+template <typename T, int MODE, int CBW, int CL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void wgrad_kernel(const WgArgs a) {
   extern __shared__ uint4 smem4[];
-  constexpr int TAPS = WgGeom<MODE>::TAPS;
+  using Geo = WgGeom<MODE>;
+  constexpr int TAPS = Geo::TAPS;
+  constexpr int TH = Geo::TH;
+  constexpr int HH = Geo::HH, HW = Geo::HW;
+  constexpr int BOXPOS = Geo::BOXPOS, HPOS = Geo::HPOS;
+  constexpr int NFI = Geo::NFI, NGI = Geo::NGI;
+  constexpr int NT = Geo::THREADS;
+  constexpr int TILE = (BOXPOS + HPOS) * 32;  // halves per buffer
   constexpr int NDBG = MODE == MODE_T2DW ? CBW : 1;
+  constexpr int WS = MODE == MODE_T2DW ? 2 : 1;  // G positions per F position along each axis
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -59,22 +73,16 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
   const int box_begin = (int)(((int64_t)split * a.nbox) / a.nsplit);
   const int box_end = (int)(((int64_t)(split + 1) * a.nbox) / a.nsplit);
 
-  constexpr int CPF = 32;  // F tile row pitch (halves)
-  const int cpg = a.GCW;   // G tile row pitch (halves)
-  const int HH = a.HH, HW = a.HW;
-  const int BOXPOS = a.TD * a.TH * 16;
-  const int HPOS = a.HD * HH * HW;
-  uint16_t* ftile = reinterpret_cast<uint16_t*>(smem4);
-  uint16_t* gtile = ftile + BOXPOS * CPF;
+  uint16_t* const tiles = reinterpret_cast<uint16_t*>(smem4);  // [2][F tile, G tile]
 
-  const int nq = a.GCW >> 2;          // channel quads per tap
+  const int nq = a.GCW >> 2;  // channel quads per tap
   const int nquads = TAPS * nq;
-  // Column blocks of this wave: this lane's quad, its tap offset and channel.
+  // This lane's column in each of the wave's blocks: its quad's tap offset and channel.
   int goff[CBW];
   bool cbok[CBW];
 #pragma unroll
   for (int q = 0; q < CBW; ++q) {
-    const int cb = wv * CBW + q;
+    const int cb = q * 8 + wv;
     cbok[q] = cb * 8 < nquads;
     const int Q = cb * 8 + 4 * h + (s & 3);
     const int tap = Q < nquads ? Q / nq : 0;
@@ -82,10 +90,10 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
     int toff = 0;
     if (MODE == MODE_K3) toff = ((tap / 9) * HH + (tap / 3) % 3) * HW + tap % 3;
     else if (MODE == MODE_T2DW) toff = ((tap >> 2) * HH + ((tap >> 1) & 1)) * HW + (tap & 1);
-    goff[q] = toff * cpg + cq * 4;
+    goff[q] = toff * 32 + cq * 4;
   }
 
-  const bool do_dbf = a.db_mode == 1 && gt == 0 && wv == 0;
+  const bool do_dbf = a.db_mode == 1 && gt == 0 && wv == 7;
   const bool do_dbg = MODE == MODE_T2DW && a.db_mode == 2 && ft == 0;
   uint4 ones;
   ones.x = ones.y = ones.z = ones.w = pack2(T::one, T::one);
@@ -104,17 +112,46 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
   const int fc0 = ft * 32;
   const int gc0 = gt * a.GCW;
   const int ggroups = a.GCW >> 3;  // 8-channel groups per G row
-  const int nf_items = BOXPOS * 4;
   const int ng_items = HPOS * ggroups;
-  const FastDiv20 divHH((uint32_t)HH);
-  const FastDiv20 divHW((uint32_t)HW);
-  const FastDiv20 divGG((uint32_t)ggroups);
-  const int th_mask = a.TH - 1;
+
+  // Staging items of this thread: item it = NT k + tid.  Code = (d, h, w, group)
+  // of the item inside its tile, 8 bits each; -1 = no such item.
+  //   F, CL: position it/4, group it%4    F, generic: group it/BOXPOS, position it%BOXPOS
+  //   G, CL: position it/ggroups, group it%ggroups   G, generic: group it/HPOS, position it%HPOS
+  int fcode[NFI], gcode[NGI];
+#pragma unroll
+  for (int k = 0; k < NFI; ++k) {
+    const int it = k * NT + tid;
+    const int pos = CL ? it >> 2 : it % BOXPOS;
+    const int cg = CL ? it & 3 : it / BOXPOS;
+    const int line = pos >> 4;
+    fcode[k] = it < BOXPOS * 4 ? ((line / TH) | ((line % TH) << 8) | ((pos & 15) << 16) | (cg << 24)) : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < NGI; ++k) {
+    const int it = k * NT + tid;
+    const int hp = CL ? it / ggroups : it % HPOS;
+    const int cg = CL ? it - hp * ggroups : it / HPOS;
+    const int t = hp / HW;
+    gcode[k] = it < ng_items ? ((t / HH) | ((t % HH) << 8) | ((hp % HW) << 16) | (cg << 24)) : -1;
+  }
   const int fs1 = (int)a.fs[1], fs2 = (int)a.fs[2], fs3 = (int)a.fs[3], fs4 = (int)a.fs[4];
   const int gs1 = (int)a.gs[1], gs2 = (int)a.gs[2], gs3 = (int)a.gs[3], gs4 = (int)a.gs[4];
-  const int fchan = s & 3;
 
-  for (int box = box_begin; box < box_end; ++box) {
+  u32x4_t pf[NFI], pg[NGI];
+  auto load8 = [&](const __amdgpu_buffer_rsrc_t& rs, bool ok, int off, int cvalid, int cs1) -> u32x4_t {
+    if (CL) return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : kOob, 0, 0));
+    u32x4_t v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rs, (ok && 2 * q < cvalid) ? off + 4 * q * cs1 : kOob, 0, 0);
+      const uint32_t hi =
+          __builtin_amdgcn_raw_buffer_load_b16(rs, (ok && 2 * q + 1 < cvalid) ? off + (4 * q + 2) * cs1 : kOob, 0, 0);
+      v[q] = lo | (hi << 16);
+    }
+    return v;
+  };
+  auto issue = [&](int box) {
     int b = box;
     const int bw = b % a.nbw;
     b /= a.nbw;
@@ -122,7 +159,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
     b /= a.nbh;
     const int bd = b % a.nbd;
     const int n = b / a.nbd;
-    const int r0d = bd * a.TD, r0h = bh * a.TH, r0w = bw * 16;
+    const int r0d = bd * Geo::TD, r0h = bh * TH, r0w = bw * 16;
     int s0d, s0h, s0w;
     if (MODE == MODE_T2DW) {
       s0d = 2 * r0d;
@@ -135,98 +172,80 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
     }
     const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (int64_t)n * a.fs[0], a.f_bytes);
     const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (int64_t)n * a.gs[0], a.g_bytes);
-
-    __syncthreads();  // the previous box is fully consumed
-    // ---- stage F box: [BOXPOS][32]
-    for (int it = tid; it < nf_items; it += 256) {
-      int pos, cg;
-      if (a.f_cl) {
-        cg = it & 3;
-        pos = it >> 2;
-      } else {
-        cg = it / BOXPOS;
-        pos = it - cg * BOXPOS;
-      }
-      const int tw = pos & 15;
-      const int rr = pos >> 4;
-      const int th = rr & th_mask;
-      const int td = rr >> a.th_log2;
-      const int gd = r0d + td, gh = r0h + th, gw = r0w + tw;
-      const int c0 = fc0 + cg * 8;
-      const bool ok = gd < a.Rd && gh < a.Rh && gw < a.Rw && c0 < a.Fc;
-      const int off = 2 * (gd * fs2 + gh * fs3 + gw * fs4 + c0 * fs1);
-      uint4 v;
-      if (a.f_cl) {
-        v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(fsrc, ok ? off : kOob, 0, 0));
-      } else {
-        uint16_t e[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-          e[q] = __builtin_amdgcn_raw_buffer_load_b16(fsrc, (ok && c0 + q < a.Fc) ? off + 2 * q * fs1 : kOob, 0, 0);
-        v = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
-      }
-      *reinterpret_cast<uint4*>(ftile + pos * CPF + cg * 8) = v;
+    for (int k = 0; k < NFI; ++k) {
+      const int c = fcode[k];
+      const int td = c & 255, th = (c >> 8) & 255, tw = (c >> 16) & 255, cg = c >> 24;
+      const int gd = r0d + td, gh = r0h + th, gw = r0w + tw, c0 = fc0 + cg * 8;
+      const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && c0 < a.Fc;
+      const int off = 2 * (gd * fs2 + gh * fs3 + gw * fs4 + c0 * fs1);
+      pf[k] = load8(fsrc, ok, off, a.Fc - c0, fs1);
     }
-    // ---- stage G box (+ halo): [HPOS][GCW]
-    for (int it = tid; it < ng_items; it += 256) {
-      int hp, cg;
-      if (a.g_cl) {
-        hp = (int)divGG.div((uint32_t)it);
-        cg = it - hp * ggroups;
-      } else {
-        cg = it / HPOS;
-        hp = it - cg * HPOS;
-      }
-      const int t = (int)divHW.div((uint32_t)hp);
-      const int hw = hp - t * HW;
-      const int hd = (int)divHH.div((uint32_t)t);
-      const int hh = t - hd * HH;
-      const int gd = s0d + hd, gh = s0h + hh, gw = s0w + hw;
-      const int c0 = gc0 + cg * 8;
-      const bool ok = (unsigned)gd < (unsigned)a.Gd && (unsigned)gh < (unsigned)a.Gh &&
+#pragma unroll
+    for (int k = 0; k < NGI; ++k) {
+      const int c = gcode[k];
+      const int hd = c & 255, hh = (c >> 8) & 255, hw = (c >> 16) & 255, cg = c >> 24;
+      const int gd = s0d + hd, gh = s0h + hh, gw = s0w + hw, c0 = gc0 + cg * 8;
+      const bool ok = c >= 0 && (unsigned)gd < (unsigned)a.Gd && (unsigned)gh < (unsigned)a.Gh &&
                       (unsigned)gw < (unsigned)a.Gw && c0 < a.Gc;
       const int off = 2 * (gd * gs2 + gh * gs3 + gw * gs4 + c0 * gs1);
-      uint4 v;
-      if (a.g_cl) {
-        v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(gsrc, ok ? off : kOob, 0, 0));
-      } else {
-        uint16_t e[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          e[q] = __builtin_amdgcn_raw_buffer_load_b16(gsrc, (ok && c0 + q < a.Gc) ? off + 2 * q * gs1 : kOob, 0, 0);
-        v = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
-      }
-      *reinterpret_cast<uint4*>(gtile + hp * cpg + cg * 8) = v;
+      pg[k] = load8(gsrc, ok, off, a.Gc - c0, gs1);
     }
-    __syncthreads();
-
-    // ---- K loop: 16 positions (one 16-wide w line) per MFMA step.
-    const int nsteps = BOXPOS >> 4;
-    for (int st = 0; st < nsteps; ++st) {
-      const int L0 = st * 16 + 8 * g + (s >> 2);
-      const int L1 = L0 + 4;
-      int grow0, grow1;
-      {
-        const int tw0 = L0 & 15, r0 = L0 >> 4;
-        const int th0 = r0 & th_mask, td0 = r0 >> a.th_log2;
-        const int tw1 = L1 & 15, r1 = L1 >> 4;
-        const int th1 = r1 & th_mask, td1 = r1 >> a.th_log2;
-        if (MODE == MODE_T2DW) {
-          grow0 = ((2 * td0) * HH + 2 * th0) * HW + 2 * tw0;
-          grow1 = ((2 * td1) * HH + 2 * th1) * HW + 2 * tw1;
-        } else {
-          grow0 = (td0 * HH + th0) * HW + tw0;
-          grow1 = (td1 * HH + th1) * HW + tw1;
-        }
+  };
+  auto commit = [&](int buf) {
+    uint16_t* ft = tiles + buf * TILE;
+    uint16_t* gtl = ft + BOXPOS * 32;
+#pragma unroll
+    for (int k = 0; k < NFI; ++k) {
+      const int c = fcode[k];
+      if (c >= 0) {
+        const int pos = ((c & 255) * TH + ((c >> 8) & 255)) * 16 + ((c >> 16) & 255);
+        *reinterpret_cast<u32x4_t*>(ft + pos * 32 + (c >> 24) * 8) = pf[k];
       }
-      grow0 *= cpg;
-      grow1 *= cpg;
-      const uint4 ffr = lds_tr_pair(ftile, L0 * CPF + 16 * h + 4 * fchan, L1 * CPF + 16 * h + 4 * fchan);
+    }
+#pragma unroll
+    for (int k = 0; k < NGI; ++k) {
+      const int c = gcode[k];
+      if (c >= 0) {
+        const int hp = ((c & 255) * HH + ((c >> 8) & 255)) * HW + ((c >> 16) & 255);
+        *reinterpret_cast<u32x4_t*>(gtl + hp * 32 + (c >> 24) * 8) = pg[k];
+      }
+    }
+  };
+
+  // Per-lane operand addresses (halves) for step 0; a step adds a line.
+  const int tw0 = 8 * g + (s >> 2);
+  const int fo = tw0 * 32 + 16 * h + 4 * (s & 3);
+  int go[CBW];
+#pragma unroll
+  for (int q = 0; q < CBW; ++q) go[q] = WS * tw0 * 32 + goff[q];
+
+  if (box_begin < box_end) {
+    issue(box_begin);
+    commit(0);
+    if (box_begin + 1 < box_end) issue(box_begin + 1);
+  }
+  for (int box = box_begin; box < box_end; ++box) {
+    const int buf = (box - box_begin) & 1;
+    __syncthreads();  // buffer buf is complete; buffer buf^1 is no longer read
+    if (box + 1 < box_end) {
+      commit(buf ^ 1);
+      if (box + 2 < box_end) issue(box + 2);  // in flight during the K loop
+    }
+    const uint16_t* ftile = tiles + buf * TILE;
+    const uint16_t* gtile = ftile + BOXPOS * 32;
+
+#pragma unroll
+    for (int st = 0; st < Geo::LINES; ++st) {
+      const int td = st / TH, th = st % TH;
+      const int frow = st * 16 * 32;
+      const int grow = ((WS * td) * HH + WS * th) * HW * 32;
+      const uint4 ffr = lds_tr_pair(ftile, fo + frow, fo + frow + 4 * 32);
       if (do_dbf) accf = mfma32<T>(ffr, ones, accf);
 #pragma unroll
       for (int q = 0; q < CBW; ++q) {
         if (!cbok[q]) continue;
-        const uint4 gfr = lds_tr_pair(gtile, grow0 + goff[q], grow1 + goff[q]);
+        const uint4 gfr = lds_tr_pair(gtile, go[q] + grow, go[q] + grow + WS * 4 * 32);
         acc[q] = mfma32<T>(ffr, gfr, acc[q]);
         if (MODE == MODE_T2DW) {
           if (do_dbg) accg[q < NDBG ? q : 0] = mfma32<T>(ones, gfr, accg[q < NDBG ? q : 0]);
@@ -241,7 +260,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
 #pragma unroll
   for (int q = 0; q < CBW; ++q) {
     if (!cbok[q]) continue;
-    const int Q = (wv * CBW + q) * 8 + (li >> 2);
+    const int Q = (q * 8 + wv) * 8 + (li >> 2);
     if (Q >= nquads) continue;
     const int tap = Q / nq;
     const int gch = gc0 + (Q - tap * nq) * 4 + (li & 3);
@@ -263,7 +282,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
 #pragma unroll
     for (int q = 0; q < NDBG; ++q) {
       if (!cbok[q]) continue;
-      const int Q = (wv * CBW + q) * 8 + (li >> 2);
+      const int Q = (q * 8 + wv) * 8 + (li >> 2);
       if (Q >= nquads) continue;
       const int tap = Q / nq;
       const int gch = gc0 + (Q - tap * nq) * 4 + (li & 3);
@@ -272,11 +291,11 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WgArgs a) {
   }
 }
 
-template <typename T, int MODE, int CBW>
+template <typename T, int MODE, int CBW, int CL>
 static void launch_wgrad_inst(const WgArgs& a, size_t lds, hipStream_t stream) {
-  auto kern = wgrad_kernel<T, MODE, CBW>;
+  auto kern = wgrad_kernel<T, MODE, CBW, CL>;
   if (lds > 65536) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(kern, dim3(a.nblocks), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3(a.nblocks), dim3(WgGeom<MODE>::THREADS), lds, stream, a);
 }
 
 }  // namespace r3c
