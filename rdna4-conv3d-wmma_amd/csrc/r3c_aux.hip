@@ -60,6 +60,58 @@ void launch_pack(int dtype, const PackArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
+// Tile = 512 positions x up to 32 channels of one sample, through LDS:
+//   load:  16-byte loads of 8 positions of one channel (lanes along positions,
+//          so each instruction reads 1 KB of a channel plane) -> LDS [c][p];
+//   store: each lane gathers 8 channels of one position from LDS and stores
+//          them as one 16-byte vector; consecutive lanes take consecutive
+//          vectors of the output, so each instruction writes 1 KB contiguously
+//          when C <= 32 (64-byte runs otherwise).
+constexpr int kLayoutTileP = 512;
+constexpr int kLayoutPitch = kLayoutTileP + 8;  // halves per LDS row (spreads banks)
+
+__global__ __launch_bounds__(256) void to_channels_last_kernel(const LayoutArgs a) {
+  __shared__ uint16_t tile[32 * kLayoutPitch];
+  const int ncb = (a.C + 31) >> 5;
+  const int64_t ntiles = (a.S + kLayoutTileP - 1) / kLayoutTileP;
+  int64_t b = blockIdx.x;
+  const int64_t pt = b % ntiles;
+  b /= ntiles;
+  const int cb = (int)(b % ncb);
+  const int64_t n = b / ncb;
+  const int c0 = cb * 32;
+  const int cw = a.C - c0 >= 32 ? 32 : a.C - c0;  // channels in this block (multiple of 8)
+  const int64_t p0 = pt * kLayoutTileP;
+  const int np = a.S - p0 >= kLayoutTileP ? kLayoutTileP : (int)(a.S - p0);  // multiple of 8
+  const int tid = threadIdx.x;
+
+  const uint16_t* src = a.src + ((size_t)n * a.C + c0) * a.S + p0;
+  const int ngrp = np >> 3;
+  for (int it = tid; it < cw * ngrp; it += 256) {
+    const int c = it / ngrp, j = it - (it / ngrp) * ngrp;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + (size_t)c * a.S + j * 8);
+    *reinterpret_cast<uint4*>(tile + c * kLayoutPitch + j * 8) = v;
+  }
+  __syncthreads();
+  const int cgw = cw >> 3;
+  uint16_t* dst = a.dst + ((size_t)n * a.S + p0) * a.C + c0;
+  for (int u = tid; u < np * cgw; u += 256) {
+    const int p = u / cgw, cg = u - (u / cgw) * cgw;
+    const uint16_t* t = tile + cg * 8 * kLayoutPitch + p;
+    uint4 v;
+    v.x = pack2(t[0], t[kLayoutPitch]);
+    v.y = pack2(t[2 * kLayoutPitch], t[3 * kLayoutPitch]);
+    v.z = pack2(t[4 * kLayoutPitch], t[5 * kLayoutPitch]);
+    v.w = pack2(t[6 * kLayoutPitch], t[7 * kLayoutPitch]);
+    *reinterpret_cast<uint4*>(dst + (size_t)p * a.C + cg * 8) = v;
+  }
+}
+
+void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.S + kLayoutTileP - 1) / kLayoutTileP * ((a.C + 31) >> 5) * a.N;
+  hipLaunchKernelGGL(to_channels_last_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+}
+
 template <typename T>
 __device__ __forceinline__ void store_elem(void* base, int64_t i, int dtype, float v) {
   (void)sizeof(T);

@@ -85,7 +85,7 @@ int ok() {
 // caller's current tag and the kernel family; collect() waits for them and
 // returns the per-launch durations.
 // ---------------------------------------------------------------------------
-enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3 };
+enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4 };
 
 struct TimingRec {
   int tag, kind;
@@ -216,6 +216,41 @@ bool vec16_ok(const void* p, const int64_t* s) {
   return (s[0] % 8 == 0) && (s[2] % 8 == 0) && (s[3] % 8 == 0) && (s[4] % 8 == 0);
 }
 
+// A fully contiguous NCDHW tensor that the NDHWC copy kernel accepts.
+bool ncdhw_copyable(const int64_t* st, int c, int d, int h, int w) {
+  const int64_t S = (int64_t)d * h * w;
+  return c % 8 == 0 && S % 8 == 0 && st[4] == 1 && st[3] == w && st[2] == (int64_t)h * w && st[1] == S &&
+         st[0] == (int64_t)c * S;
+}
+
+// Element strides (n, c, d, h, w) of the NDHWC copy.
+void channels_last_strides(int64_t* st, int c, int d, int h, int w) {
+  st[1] = 1;
+  st[4] = c;
+  st[3] = (int64_t)w * c;
+  st[2] = (int64_t)h * w * c;
+  st[0] = (int64_t)d * h * w * c;
+}
+
+int64_t tensor_bytes(int n, int c, int d, int h, int w) { return (int64_t)n * c * d * h * w * 2; }
+
+int copy_to_channels_last(const void* src, void* dst, int n, int c, int d, int h, int w, hipStream_t s) {
+  if ((reinterpret_cast<uintptr_t>(src) & 15) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15) != 0)
+    return fail(R3C_INVALID, "layout copy needs 16-byte aligned tensors");
+  LayoutArgs la;
+  la.src = static_cast<const uint16_t*>(src);
+  la.dst = static_cast<uint16_t*>(dst);
+  la.S = (int64_t)d * h * w;
+  la.C = c;
+  la.N = n;
+  {
+    TimedLaunch tl(KIND_LAYOUT, s);
+    launch_to_channels_last(la, s);
+    tl.end();
+  }
+  return check_launch("layout copy");
+}
+
 // Bytes of one sample reachable from its base through `strides` (0 if too large
 // for 32-bit buffer offsets).
 uint32_t sample_bytes(const int64_t* st, int c, int d, int h, int w) {
@@ -235,6 +270,7 @@ struct RowPlan {
   PackArgs pk;
   size_t lds;
   int64_t wpk_bytes;
+  int64_t copy_bytes;  // > 0: the source is first copied to NDHWC in the workspace
 };
 
 int pick_ck(int cs) { return cs <= 8 ? 8 : cs <= 16 ? 16 : cs <= 24 ? 24 : 32; }
@@ -310,6 +346,14 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   (void)sc;
   a.Cs = cs;
   a.Sd = sdd; a.Sh = sh; a.Sw = sw;
+  // A low-channel NCDHW source of a k=3 pass is copied to NDHWC first: its
+  // channel-contiguous staging is faster than strided staging by more than the
+  // copy costs (two bytes read and written per element).
+  p.copy_bytes = 0;
+  if (p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
+    p.copy_bytes = align256(tensor_bytes(d->n, cs, sdd, sh, sw));
+    channels_last_strides(a.ss, cs, sdd, sh, sw);
+  }
   a.src_bytes = sample_bytes(a.ss, cs, sdd, sh, sw);
   // Channel-contiguous sources are staged by direct-to-LDS 16-byte loads;
   // others by 8 scalar loads per slot through registers.
@@ -389,9 +433,9 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   plan_row(d, op, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
   if (p.a.src_bytes == 0) return fail(R3C_UNSUPPORTED, "one input sample exceeds 1 GiB (32-bit buffer offsets)");
-  if (ws_bytes < align256(p.wpk_bytes))
+  if (ws_bytes < align256(p.wpk_bytes) + p.copy_bytes)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes,
-                (long long)align256(p.wpk_bytes));
+                (long long)(align256(p.wpk_bytes) + p.copy_bytes));
   if (!src || !w || !dst || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
   int rc = check_device();
   if (rc) return rc;
@@ -406,6 +450,12 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   }
   rc = check_launch("weight pack");
   if (rc) return rc;
+  if (p.copy_bytes) {
+    void* copy = static_cast<char*>(ws) + align256(p.wpk_bytes);
+    rc = copy_to_channels_last(src, copy, d->n, p.a.Cs, p.a.Sd, p.a.Sh, p.a.Sw, s);
+    if (rc) return rc;
+    src = copy;
+  }
   RowArgs a = p.a;
   a.src = static_cast<const uint16_t*>(src);
   a.wpk = static_cast<const uint16_t*>(ws);
@@ -435,6 +485,7 @@ struct WgPlan {
   WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
+  int64_t fcopy_bytes, gcopy_bytes;  // > 0: that operand is first copied to NDHWC
 };
 
 void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
@@ -457,6 +508,20 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
     a.pd = d->pad_d; a.ph = d->pad_h; a.pw = d->pad_w;
     memcpy(a.fs, d->y_strides, sizeof a.fs);
     memcpy(a.gs, d->x_strides, sizeof a.gs);
+  }
+  // NCDHW operands of the k=3 pass are copied to NDHWC first: the tiles are
+  // [position][channel], which strided staging fills slowly, and the pass does
+  // enough arithmetic per byte to pay for the copy.  The memory-bound k=1 and
+  // ConvTranspose passes stage strided operands directly.
+  p.fcopy_bytes = p.gcopy_bytes = 0;
+  const bool copy_ok = p.mode == MODE_K3;
+  if (copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
+    p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
+    channels_last_strides(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
+  }
+  if (copy_ok && ncdhw_copyable(a.gs, a.Gc, a.Gd, a.Gh, a.Gw)) {
+    p.gcopy_bytes = align256(tensor_bytes(d->n, a.Gc, a.Gd, a.Gh, a.Gw));
+    channels_last_strides(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   }
   a.f_bytes = sample_bytes(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
   a.g_bytes = sample_bytes(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
@@ -509,7 +574,7 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
   if (p.a.f_bytes == 0 || p.a.g_bytes == 0)
     return fail(R3C_UNSUPPORTED, "one sample exceeds 1 GiB (32-bit buffer offsets)");
-  const int64_t need = p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
+  const int64_t need = p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
@@ -522,6 +587,19 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   WgArgs a = p.a;
   a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
+  {
+    char* copies = static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
+    if (p.fcopy_bytes) {
+      rc = copy_to_channels_last(a.fsrc, copies, d->n, a.Fc, a.Rd, a.Rh, a.Rw, s);
+      if (rc) return rc;
+      a.fsrc = reinterpret_cast<const uint16_t*>(copies);
+    }
+    if (p.gcopy_bytes) {
+      rc = copy_to_channels_last(a.gsrc, copies + p.fcopy_bytes, d->n, a.Gc, a.Gd, a.Gh, a.Gw, s);
+      if (rc) return rc;
+      a.gsrc = reinterpret_cast<const uint16_t*>(copies + p.fcopy_bytes);
+    }
+  }
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
   // Channel-contiguous 16-byte staging when both operands allow it, else 8 scalar loads per slot.
@@ -562,14 +640,14 @@ int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   RowPlan p;
   plan_row(d, op, p);
-  return align256(p.wpk_bytes);
+  return align256(p.wpk_bytes) + p.copy_bytes;
 }
 
 int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   WgPlan p;
   plan_wgrad(d, transpose, p);
-  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
+  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
 }
 
 std::mutex g_dev_mu;

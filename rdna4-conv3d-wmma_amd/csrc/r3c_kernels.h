@@ -116,12 +116,22 @@ struct PackArgs {
   int64_t total;
 };
 
+// NCDHW -> NDHWC copy of a fully contiguous tensor (C % 8 == 0, S % 8 == 0,
+// both pointers 16-byte aligned): dst[n][s][c] = src[n][c][s], s = (d, h, w).
+struct LayoutArgs {
+  const uint16_t* src;
+  uint16_t* dst;
+  int64_t S;     // positions per channel plane
+  int32_t C, N;
+};
+
 // Host launchers (return false when no instantiation matches).
 // `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
                 hipStream_t stream);
 bool launch_wgrad(int dtype, int mode, int cbw, int cl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
+void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
 // One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 
