@@ -391,7 +391,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   // for two workgroups per CU (8 waves), else the one with the most room.
   //   wfull: every chunk's weights resident (only with a single column tile)
   //   nbuf 2: double-buffered stages, one barrier per stage; 1: two barriers
-  const int64_t fixed = 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4 + (int64_t)nstep * 2 * 4;
+  const int64_t fixed = 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4;
   const int64_t act1 = (int64_t)g8 * a.CGS * 16;
   struct Opt { int wfull, nbuf; };
   static const Opt opts2[] = {{1, 2}, {0, 2}, {1, 1}, {0, 1}};

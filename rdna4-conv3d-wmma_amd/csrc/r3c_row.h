@@ -30,6 +30,8 @@
 // conv3d_wmma.py:372-444), K1 fwd (328-369), ConvTranspose fwd scatter
 // (793-860) and ConvTranspose dX gather (863-931).
 #pragma once
+#include <type_traits>
+
 #include "r3c_device.h"
 #include "r3c_kernels.h"
 
@@ -43,6 +45,17 @@ struct FastDiv20 {
 };
 
 constexpr int kOob = 0x7fffff00;  // byte offset past any num_records: the load returns 0
+
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS accesses
+// (lgkmcnt 0; vmcnt and expcnt left at their maxima) and not for its global
+// loads, so register prefetches stay in flight across it.  __syncthreads()
+// would also drain vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
 
 template <int MODE>
 struct RowGeom {
@@ -86,16 +99,15 @@ __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
 
 // LDS: act[2][G8][HPAD] 16-byte slots (double-buffered tile, HPAD = HPOS rounded
 // up to 16), the weight fragments (all of K when WF, else two chunk buffers of
-// NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB), the bias
-// table (fp32, one per packed column) and the tap table.
+// NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB) and the
+// bias table (fp32, one per packed column).
 //
 // Pipeline: one stage = one 8-channel (16 for single-tap modes) chunk of one
-// job.  Stage t+1's activations (and, without WF, its weights) are loaded into
-// registers while stage t computes from LDS, then written to the other buffer;
-// one barrier per stage.  Only the resident weights (WF) use direct-to-LDS
-// loads, once, before the loop: the compiler makes every LDS read that follows
-// an in-flight direct-to-LDS load wait for it, which would serialise a
-// per-stage DMA with the compute it is meant to overlap.
+// job.  Stage t+DIST's activations (DIST = 2 where the registers allow, else
+// 1) and, without WF, stage t+1's weights are loaded into registers while
+// stage t computes from LDS, and written to LDS at the start of their stage;
+// one barrier per stage with double buffers.  The barrier waits for LDS
+// traffic only, so the register prefetches stay in flight across it.
 //
 // Epilogue: a wave converts each 32 x 32 C tile (plus bias) to 16-bit and
 // writes it to its scratch as [column][position] with 8-byte writes, then
@@ -104,7 +116,11 @@ __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
 // ds_read_tr16_b64, 8 consecutive channels of one position per lane when
 // channels are contiguous (NDHWC) -- so every global store is 16 bytes.
 template <typename T, int MODE, int NB, int CL, int WF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void row_kernel(const RowArgs a) {
+// A 27-tap chunk with three column blocks of per-stage weights needs more than
+// half the register file; those instantiations run one wave per SIMD.
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 8))) void row_kernel(
+    const RowArgs a) {
   extern __shared__ uint4 smem4[];
   constexpr int TAPS = RowGeom<MODE>::TAPS;
   constexpr int HW = RowGeom<MODE>::HW;
@@ -132,14 +148,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   uint16_t* scr = reinterpret_cast<uint16_t*>(wts + wslots) + wv * 1024;
   float* btab = reinterpret_cast<float*>(wts + wslots + 4 * 128);
   const int nbcol = a.nbt_pad * 32;
-  int* ktab = reinterpret_cast<int*>(btab + nbcol);
 
   // Contiguous job range of this workgroup; a job is (box, column tile).
   const int j0 = (int)(((int64_t)blockIdx.x * a.njobs) / gridDim.x);
   const int j1 = (int)(((int64_t)(blockIdx.x + 1) * a.njobs) / gridDim.x);
   if (j0 >= j1) return;
 
-  for (int kg = tid; kg < NSTEP * 2; kg += 256) {
+  // Slot offset of k group 2s + g (tap, channel group) for each step s of this
+  // lane's half; held in registers so the fully unrolled K loop issues every
+  // LDS read without waiting on a table.
+  int kof[NSTEP];
+#pragma unroll
+  for (int st = 0; st < NSTEP; ++st) {
+    const int kg = 2 * st + g;
     int off = 0;  // K padding: the row's own slot, times zero weights
     if (kg < TAPS * G8) {
       const int tap = kg / G8, cg = kg - (kg / G8) * G8;
@@ -147,7 +168,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       else if (MODE == MODE_T2DX) off = ((tap >> 2) * HH + ((tap >> 1) & 1)) * HW + (tap & 1) * 32;
       off += cg * HPAD;
     }
-    ktab[kg] = off;
+    kof[st] = off;
   }
   for (int c = tid; c < nbcol; c += 256) {
     float bv = 0.f;
@@ -180,23 +201,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     }
   }
   const int ss1 = (int)a.ss[1], ss2 = (int)a.ss[2], ss3 = (int)a.ss[3], ss4 = (int)a.ss[4];
-  uint4 pfa[G8 * MAXK];
+  // Activation prefetch depth in stages: two where the registers allow it.
+  constexpr int DIST = (NB == 1 || (NB == 2 && WF) || (MODE == MODE_K3 && NB == 3 && !WF)) ? 2 : 1;
+  uint4 pfa[DIST][G8 * MAXK];
   u32x4_t pfw[WIT];
 
-  auto box_of = [&](int job, int& n, int& bd, int& bh, int& bw) {
+  // A stage cursor: (chunk, column tile, box w, h, d, sample), advanced with
+  // carries so the per-stage index math is a few scalar adds (the divisions
+  // happen once per workgroup).
+  struct Cursor {
+    int chunk, ct, bw, bh, bd, n;
+  };
+  auto cursor_at = [&](int job) {
+    Cursor c;
+    c.chunk = 0;
+    c.ct = job % a.n_ctiles;
     int b = job / a.n_ctiles;
-    bw = b % a.nbw;
+    c.bw = b % a.nbw;
     b /= a.nbw;
-    bh = b % a.nbh;
+    c.bh = b % a.nbh;
     b /= a.nbh;
-    bd = b % a.nbd;
-    n = b / a.nbd;
+    c.bd = b % a.nbd;
+    c.n = b / a.nbd;
+    return c;
+  };
+  auto advance = [&](Cursor& c) {
+    if (++c.chunk < a.nchunks) return;
+    c.chunk = 0;
+    if (++c.ct < a.n_ctiles) return;
+    c.ct = 0;
+    if (++c.bw < a.nbw) return;
+    c.bw = 0;
+    if (++c.bh < a.nbh) return;
+    c.bh = 0;
+    if (++c.bd < a.nbd) return;
+    c.bd = 0;
+    ++c.n;
   };
   const uint4* wsrc = reinterpret_cast<const uint4*>(a.wpk);
-  // Issue the loads of stage (job, chunk) into registers.
-  auto issue = [&](int job, int chunk) {
-    int n, bd, bh, bw;
-    box_of(job, n, bd, bh, bw);
+  // Issue the activation loads of stage `cur` into register slot `slot`.
+  auto issue_act = [&](const Cursor& cur, int slot) {
+    const int n = cur.n, bd = cur.bd, bh = cur.bh, bw = cur.bw, chunk = cur.chunk;
     int s0d, s0h, s0w;
     if (MODE == MODE_K3 || MODE == MODE_K1) {
       s0d = bd * a.TD - a.pd;
@@ -223,7 +268,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
                         (unsigned)gw < (unsigned)a.Sw && c0 < a.Cs;
         const int off = 2 * (gd * ss2 + gh * ss3 + gw * ss4 + c0 * ss1);
         if (CL) {
-          pfa[cg * MAXK + k] =
+          pfa[slot][cg * MAXK + k] =
               __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, ok ? off : kOob, 0, 0));
         } else {
           uint32_t wd[4];
@@ -235,12 +280,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
                 src, (ok && c0 + 2 * q + 1 < a.Cs) ? off + (4 * q + 2) * ss1 : kOob, 0, 0);
             wd[q] = lo | (hi << 16);
           }
-          pfa[cg * MAXK + k] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+          pfa[slot][cg * MAXK + k] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
         }
       }
     }
-    if (!WF) {
-      const int ct = job % a.n_ctiles;
+  };
+  // Issue the weight loads of stage `cur` (per-stage weights only).
+  auto issue_w = [&](const Cursor& cur) {
+    {
+      const int ct = cur.ct, chunk = cur.chunk;
 #pragma unroll
       for (int i = 0; i < WIT; ++i) {
         // uint4 index inside the chunk's fragments; the tail of the last
@@ -252,18 +300,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       }
     }
   };
-  auto commit = [&](int buf) {
+  auto commit_act = [&](int slot, int buf) {
 #pragma unroll
     for (int cg = 0; cg < G8; ++cg)
 #pragma unroll
       for (int k = 0; k < MAXK; ++k)
-        if (k * 256 + tid < HPOS) act[buf * ABUF + cg * HPAD + k * 256 + tid] = pfa[cg * MAXK + k];
-    if (!WF) {
+        if (k * 256 + tid < HPOS) act[buf * ABUF + cg * HPAD + k * 256 + tid] = pfa[slot][cg * MAXK + k];
+  };
+  auto commit_w = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < WIT; ++i) {
-        const int e = i * 256 + tid;
-        if (e < WFRAG) *reinterpret_cast<u32x4_t*>(wts + buf * WFRAG + e) = pfw[i];
-      }
+    for (int i = 0; i < WIT; ++i) {
+      const int e = i * 256 + tid;
+      if (e < WFRAG) *reinterpret_cast<u32x4_t*>(wts + buf * WFRAG + e) = pfw[i];
     }
   };
 
@@ -275,49 +323,75 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
 
-  if (WF) {  // every chunk's weights, once, straight into LDS
-    for (int c = 0; c < a.nchunks; ++c)
-      for (int f = wv; f < NSTEP * NB; f += 4) {
-        const int s = f / NB, nb = f - (f / NB) * NB;
-        const uint4* p = wsrc + (((size_t)c * NSTEP + s) * a.nbt_pad + nb) * 64 + lane;
-        __builtin_amdgcn_global_load_lds((const void*)p, (lds_void_t*)(wts + c * WFRAG + f * 64), 16, 0, 0);
-      }
+  if (WF) {  // every chunk's weights, once (a single column tile: fragments are contiguous)
+    const u32x4_t* wsrc4 = reinterpret_cast<const u32x4_t*>(a.wpk);
+    for (int e = tid; e < a.nchunks * WFRAG; e += 256)
+      *reinterpret_cast<u32x4_t*>(wts + e) = wsrc4[e];
   }
-  int job = j0, chunk = 0, t = 0;
-  issue(job, 0);
-  while (true) {
+  // Stage t walks (job, chunk) from (j0, 0).  Activations are loaded DIST
+  // stages ahead, per-stage weights one stage ahead; `cc` is the stage being
+  // computed, `ca` / `cw` the next activation / weight stage to issue.
+  const int nstage = (j1 - j0) * a.nchunks;
+  Cursor cc = cursor_at(j0);
+  Cursor ca = cc, cw = cc;
+  issue_act(ca, 0);
+  advance(ca);
+  if (!WF) {
+    issue_w(cw);
+    advance(cw);
+  }
+  if (DIST == 2 && nstage > 1) {
+    issue_act(ca, DIST - 1);
+    advance(ca);
+  }
+  // With two slots the loop is unrolled by two so each slot is a fixed set of
+  // registers (no copies of loads still in flight).
+  auto run_stage = [&](int t, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    const int chunk = cc.chunk;
     const int buf = nbuf == 2 ? (t & 1) : 0;
-    commit(buf);
-    __syncthreads();
-    int njob = job, nchunk = chunk + 1;
-    if (nchunk == a.nchunks) {
-      nchunk = 0;
-      ++njob;
+    commit_act(SL, buf);
+    if (!WF) commit_w(buf);
+    lds_barrier();
+    if (t + DIST < nstage) {
+      issue_act(ca, SL);  // in flight during the next DIST stages
+      advance(ca);
     }
-    const bool more = njob < j1;
-    if (more) issue(njob, nchunk);  // in flight while this stage computes
+    if (!WF && t + 1 < nstage) {
+      issue_w(cw);
+      advance(cw);
+    }
 
-    const int ct = job % a.n_ctiles;
+    const int ct = cc.ct;
     const uint4* wc = WF ? wts + chunk * WFRAG : wts + buf * WFRAG;
     const uint4* ab = act + buf * ABUF;
-#pragma unroll 2
+    // Fragments are read PD steps ahead of the MFMAs that use them (two steps
+    // when a step has only MB MFMAs, fewer than an LDS read's latency covers).
+    constexpr int PD = NB == 1 ? 2 : 1;
+    uint4 bfr[PD + 1][NB], afr[PD + 1][MB];
+    auto read_step = [&](int st, int slot) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bfr[slot][nb] = wc[(st * NB + nb) * 64 + lane];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) afr[slot][mb] = ab[rowbase[mb] + kof[st]];
+    };
+#pragma unroll
+    for (int st = 0; st < PD; ++st)
+      if (st < NSTEP) read_step(st, st);
+#pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
-      const int koff = ktab[s * 2 + g];
-      uint4 bfr[NB];
+      const int cur = s % (PD + 1);
+      if (s + PD < NSTEP) read_step(s + PD, (s + PD) % (PD + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) bfr[nb] = wc[(s * NB + nb) * 64 + lane];
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const uint4 afr = ab[rowbase[mb] + koff];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr, bfr[nb], acc[mb][nb]);
-      }
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr[cur][mb], bfr[cur][nb], acc[mb][nb]);
     }
 
     if (chunk == a.nchunks - 1) {
       // Epilogue: lane (g, i) holds rows 8q + 4g + r (w positions) of column i.
-      int n, bd, bh, bw;
-      box_of(job, n, bd, bh, bw);
+      const int n = cc.n, bd = cc.bd, bh = cc.bh, bw = cc.bw;
       const int r0d = bd * a.TD, r0h = bh * a.TH, r0w = bw * 32;
       const int64_t* sd = a.sd;
       uint16_t* dstn = a.dst + (int64_t)n * sd[0];
@@ -422,11 +496,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
           for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
       }
     }
-    if (!more) break;
-    if (nbuf == 1) __syncthreads();  // every wave is done with the buffers the next commit overwrites
-    job = njob;
-    chunk = nchunk;
-    ++t;
+    if (nbuf == 1 && t + 1 < nstage) lds_barrier();  // the next commit overwrites the buffers
+    advance(cc);
+  };
+  if (DIST == 2) {
+    for (int t = 0; t < nstage; t += 2) {
+      run_stage(t, std::integral_constant<int, 0>{});
+      if (t + 1 < nstage) run_stage(t + 1, std::integral_constant<int, DIST - 1>{});
+    }
+  } else {
+    for (int t = 0; t < nstage; ++t) run_stage(t, std::integral_constant<int, 0>{});
   }
 }
 
