@@ -18,7 +18,11 @@ Also reported on the same JSON line:
   cpu_baseline  the reference's CPU path (Conv3dWmma on CPU tensors ->
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc]
+  unet3d        BASELINE config 5: ms per AMP training step (and per sample) of the
+                base=24 UNet3D at batch 4 built with this package's layers, the same
+                with stock nn.Conv3d / nn.ConvTranspose3d, and the largest loss gap.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
 """
 from __future__ import annotations
 
@@ -104,6 +108,112 @@ def cpu_baseline(budget_s: float = 20.0):
     }
 
 
+def _unet_block(cin, cout, conv):
+    import torch.nn as nn
+    return nn.Sequential(
+        conv(cin, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
+        conv(cout, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
+    )
+
+
+def build_unet3d(conv, tr, base=24, cin=1, classes=2):
+    """UNet3D of BASELINE config 5: 4 levels (base, 2, 4, 8 x base channels),
+    two (3x3x3 conv + BatchNorm + ReLU) per block, MaxPool3d(2) down,
+    ConvTranspose3d k2s2 up with skip concat, 1x1x1 head to `classes`.
+    `conv` / `tr` are the Conv3d / ConvTranspose3d classes to build with (the
+    reference's factory pattern, benches/unet_e2e.py:13-32)."""
+    import torch
+    import torch.nn as nn
+
+    ch = [base, 2 * base, 4 * base, 8 * base]
+
+    class UNet3D(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.enc = nn.ModuleList([_unet_block(cin, ch[0], conv), _unet_block(ch[0], ch[1], conv),
+                                      _unet_block(ch[1], ch[2], conv), _unet_block(ch[2], ch[3], conv)])
+            self.pool = nn.MaxPool3d(2)
+            self.up = nn.ModuleList([tr(ch[3], ch[2], 2, stride=2), tr(ch[2], ch[1], 2, stride=2),
+                                     tr(ch[1], ch[0], 2, stride=2)])
+            self.dec = nn.ModuleList([_unet_block(2 * ch[2], ch[2], conv), _unet_block(2 * ch[1], ch[1], conv),
+                                      _unet_block(2 * ch[0], ch[0], conv)])
+            self.head = conv(ch[0], classes, 1)
+
+        def forward(self, x):
+            skips = []
+            for i, blk in enumerate(self.enc):
+                x = blk(x)
+                if i < 3:
+                    skips.append(x)
+                    x = self.pool(x)
+            for up, dec, skip in zip(self.up, self.dec, reversed(skips)):
+                x = dec(torch.cat([up(x), skip], dim=1))
+            return self.head(x)
+
+    return UNet3D()
+
+
+def unet3d_train(conv, tr, base, x, labels, steps, warmup):
+    """AMP bf16 training of build_unet3d(conv, tr, base) on (x, labels):
+    cross-entropy, Adam(lr=1e-3).  Weights are seeded (seed 1) before the build,
+    so two calls with different layer classes start from identical weights.
+    Returns (ms per timed step, losses of every step in order)."""
+    import torch
+    import torch.nn as nn
+    torch.manual_seed(1)
+    net = build_unet3d(conv, tr, base).to(x.device)
+    opt = torch.optim.Adam(net.parameters(), lr=1e-3)
+    loss_fn = nn.CrossEntropyLoss()
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = net(x)
+            loss = loss_fn(y, labels)
+        loss.backward()
+        opt.step()
+        return loss.detach()
+
+    losses = [step() for _ in range(warmup)]
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        losses.append(step())
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(1, steps)
+    del net, opt
+    return ms, [float(v) for v in losses]
+
+
+def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
+    """this package's layers vs stock nn.Conv3d / nn.ConvTranspose3d."""
+    import torch
+    import torch.nn as nn
+    from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(batch, 1, 64, 128, 128, generator=g).cuda()
+    labels = torch.randint(0, 2, (batch, 64, 128, 128), generator=torch.Generator().manual_seed(3)).cuda()
+    ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup)
+    torch.cuda.empty_cache()
+    ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup)
+    torch.cuda.empty_cache()
+    return {
+        "config": f"base={base} b{batch} x[{batch},1,64,128,128] AMP bf16, CrossEntropy, Adam lr 1e-3, NCDHW",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_w, 3),
+        "ms_per_sample": round(ms_w / batch, 3),
+        "stock_ms_per_step": round(ms_s, 3),
+        "speedup_vs_stock": round(ms_s / ms_w, 3),
+        "max_abs_dloss": round(max(abs(a - b) for a, b in zip(loss_w, loss_s)), 6),
+        "final_loss": round(loss_w[-1], 6),
+        "stock_final_loss": round(loss_s[-1], 6),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +222,7 @@ def main() -> int:
     ap.add_argument("--layout", choices=("ncdhw", "ndhwc"), default="ncdhw")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--unet-steps", type=int, default=40, help="UNet3D config-5 timed steps (0 skips it)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -226,10 +337,12 @@ def main() -> int:
         "flops_per_launch": dfl,
     }
 
+    del layers
+    torch.cuda.empty_cache()
+    unet = unet3d_bench(args.unet_steps, 3) if args.unet_steps > 0 else None
+
     cpu = None
     if not args.no_cpu_baseline:
-        del layers
-        torch.cuda.empty_cache()
         cpu = cpu_baseline(args.cpu_budget)
 
     line = {
@@ -258,6 +371,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "passes": passes,
+        "unet3d": unet,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
