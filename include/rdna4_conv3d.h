@@ -23,8 +23,13 @@
  *     own fallback, e.g. F.conv3d), R3C_INVALID (2: bad argument) or
  *     R3C_HIP_ERROR (3: a HIP launch failed).  On any non-zero return,
  *     r3c_last_error() describes the problem (thread-local string).
- *   - Calls are re-entrant; the only global state is a thread-safe cache of
- *     per-device properties.
+ *   - Calls are re-entrant.  Global state: a thread-safe cache of per-device
+ *     properties, and the optional launch-timing records (r3c_timing_*),
+ *     which are off unless enabled and are guarded by a mutex.
+ *   - The workspace holds the packed weight, dW partial sums and, for some
+ *     NCDHW inputs, an NDHWC copy of an operand; its size depends on the
+ *     descriptor only (strides included), so one query serves every call
+ *     with the same descriptor.
  *
  * Which reference interface each entry replaces is cited per function
  * (paths relative to the reference repository root).
