@@ -137,7 +137,8 @@ int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* desc, const void* x,
  * time.perf_counter, benches/isolated.py:26-34).  While enabled, each kernel
  * launch is bracketed by HIP events on its own launch stream and tagged with
  * the calling thread's current tag and a kernel family
- * (0 weight pack, 1 row kernel, 2 weight-gradient kernel, 3 split reduce).
+ * (0 weight pack, 1 row kernel, 2 weight-gradient kernel, 3 split reduce,
+ * 4 NCDHW-to-NDHWC copy, 5 row-kernel split-K epilogue pass).
  * r3c_timing_collect waits for the recorded events, writes up to max_records
  * (tag, kind, milliseconds) triples, clears the records and returns how many
  * launches were recorded. */

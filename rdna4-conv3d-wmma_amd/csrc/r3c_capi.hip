@@ -85,7 +85,7 @@ int ok() {
 // caller's current tag and the kernel family; collect() waits for them and
 // returns the per-launch durations.
 // ---------------------------------------------------------------------------
-enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4 };
+enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4, KIND_SPLIT_EPI = 5 };
 
 struct TimingRec {
   int tag, kind;
@@ -139,6 +139,7 @@ struct TimedLaunch {
 };
 
 constexpr int64_t kMaxLds = 160 * 1024;
+constexpr int64_t kSplitTarget = 512;          // row-kernel jobs to aim for (two workgroups per CU)
 constexpr int kNumCUs = 256;                   // MI355X compute units
 constexpr int64_t kMaxPartialBytes = 96ll << 20;
 
@@ -271,6 +272,8 @@ struct RowPlan {
   size_t lds;
   int64_t wpk_bytes;
   int64_t copy_bytes;  // > 0: the source is first copied to NDHWC in the workspace
+  int64_t part_bytes;  // split-K partial tiles (0 without split)
+  int64_t ntiles;      // output tiles (box, column tile)
 };
 
 int pick_ck(int cs) { return cs <= 8 ? 8 : cs <= 16 ? 16 : cs <= 24 ? 24 : 32; }
@@ -391,7 +394,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   // for two workgroups per CU (8 waves), else the one with the most room.
   //   wfull: every chunk's weights resident (only with a single column tile)
   //   nbuf 2: double-buffered stages, one barrier per stage; 1: two barriers
-  const int64_t fixed = 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4;
+  const int64_t fixed = 4 * 2048 + (int64_t)a.nbt_pad * 32 * 4 + 16;
   const int64_t act1 = (int64_t)g8 * a.CGS * 16;
   struct Opt { int wfull, nbuf; };
   static const Opt opts2[] = {{1, 2}, {0, 2}, {1, 1}, {0, 1}};
@@ -425,6 +428,23 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   pk.mode = p.mode | (op == OP_CONV_DX ? 16 : 0);
   pk.total = (int64_t)a.nchunks * nstep * a.nbt_pad * 64 * 8;
   p.wpk_bytes = pk.total * 2;
+
+  // Split K over the source-channel chunks when there are fewer output tiles
+  // than CUs: the largest divisor of nchunks that keeps jobs <= kSplitTarget
+  // (two workgroups per CU).  With a tile per CU already, the partial-sum
+  // traffic and the epilogue pass cost more than the extra parallelism gains
+  // (measured).  Only the Conv3d modes, whose K is long.
+  p.ntiles = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
+  int split = 1;
+  if ((p.mode == MODE_K3 || p.mode == MODE_K1) && p.ntiles < kNumCUs) {
+    const int64_t want = (kSplitTarget + p.ntiles - 1) / p.ntiles;
+    for (int sp = 2; sp <= a.nchunks && sp <= want; ++sp)
+      if (a.nchunks % sp == 0) split = sp;
+  }
+  a.nsplit = split;
+  a.cps = a.nchunks / split;
+  const int mb = p.mode == MODE_T2DX ? 1 : 2;
+  p.part_bytes = split > 1 ? align256(p.ntiles * split * 4 * mb * p.nb * 16 * 64 * 4) : 0;
 }
 
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
@@ -433,13 +453,15 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   plan_row(d, op, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
   if (p.a.src_bytes == 0) return fail(R3C_UNSUPPORTED, "one input sample exceeds 1 GiB (32-bit buffer offsets)");
-  if (ws_bytes < align256(p.wpk_bytes) + p.copy_bytes)
-    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes,
-                (long long)(align256(p.wpk_bytes) + p.copy_bytes));
+  const int64_t need = align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;
+  if (ws_bytes < need)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!src || !w || !dst || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
   int rc = check_device();
   if (rc) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* wsb = static_cast<char*>(ws);
+  float* part = p.part_bytes ? reinterpret_cast<float*>(wsb + align256(p.wpk_bytes) + p.copy_bytes) : nullptr;
   PackArgs pk = p.pk;
   pk.w = static_cast<const uint16_t*>(w);
   pk.out = static_cast<uint16_t*>(ws);
@@ -461,20 +483,31 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   a.wpk = static_cast<const uint16_t*>(ws);
   a.bias = static_cast<const uint16_t*>(bias);
   a.dst = static_cast<uint16_t*>(dst);
-  a.src_cl = p.cl;
-  if (p.cl && (reinterpret_cast<uintptr_t>(src) & 15) != 0) return fail(R3C_INVALID, "source not 16-byte aligned");
-  const int64_t jobs = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
+  // 16-byte staging needs a 16-byte aligned source; otherwise stage by scalars.
+  const int cl = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? p.cl : 0;
+  a.src_cl = cl;
+  a.part = part;
+  a.ntiles = (int32_t)p.ntiles;
+  a.phase = 0;
+  const int64_t jobs = p.ntiles * a.nsplit;
   if (jobs >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
   a.njobs = (int32_t)jobs;
   // The launcher sizes the grid to the resident capacity (CUs x workgroups
   // per CU from the occupancy query); workgroups take contiguous job ranges.
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = launch_row(d->dtype, p.mode, p.nb, p.cl, a.wfull, a, t_cus, p.lds, s);
+  const bool launched = launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
   tl.end();
   if (!launched)
     return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d cl %d", p.mode, p.ck, p.nb,
                 p.cl);
-  return check_launch("row kernel");
+  rc = check_launch("row kernel");
+  if (rc || a.nsplit == 1) return rc;
+  // Split K: the epilogue pass adds each tile's split partial sums in split order.
+  a.phase = 1;
+  TimedLaunch te(KIND_SPLIT_EPI, s);
+  launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
+  te.end();
+  return check_launch("row kernel epilogue pass");
 }
 
 // ---------------------------------------------------------------------------
@@ -640,7 +673,7 @@ int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   RowPlan p;
   plan_row(d, op, p);
-  return align256(p.wpk_bytes) + p.copy_bytes;
+  return align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;
 }
 
 int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {

@@ -46,7 +46,11 @@ struct RowArgs {
   int32_t wfull;           // 1: every chunk's weights stay resident in LDS
   int32_t nbuf;            // 2: double-buffered stages; 1: single buffers, two barriers per stage
   int32_t src_cl;          // 1: channel-contiguous 16-byte source loads are legal
-  int32_t njobs;           // (box, column tile) jobs; workgroups stride over them
+  int32_t njobs;           // (box, column tile, split) jobs; workgroups take contiguous ranges
+  int32_t nsplit, cps;     // K splits per output tile and chunks per split (nchunks = nsplit * cps)
+  float* part;             // nsplit > 1: fp32 partial tiles [tile][split][wave][MB*NB*16][64]
+  int32_t ntiles;          // output tiles (box, column tile)
+  int32_t phase;           // 0: main pass; 1: split-K epilogue pass, one workgroup per tile
 };
 
 // Weight-gradient box geometry, fixed per mode: TD x TH lines of 16

@@ -99,8 +99,8 @@ __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
 
 // LDS: act[2][G8][HPAD] 16-byte slots (double-buffered tile, HPAD = HPOS rounded
 // up to 16), the weight fragments (all of K when WF, else two chunk buffers of
-// NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB) and the
-// bias table (fp32, one per packed column).
+// NSTEP x NB fragments), the per-wave epilogue scratch (4 x 2 KB) and the bias
+// table (fp32, one per packed column).
 //
 // Pipeline: one stage = one 8-channel (16 for single-tap modes) chunk of one
 // job.  Stage t+DIST's activations (DIST = 2 where the registers allow, else
@@ -201,6 +201,14 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
     }
   }
   const int ss1 = (int)a.ss[1], ss2 = (int)a.ss[2], ss3 = (int)a.ss[3], ss4 = (int)a.ss[4];
+  // Byte offset of each staging slot relative to the tile origin, so a stage
+  // forms each address with one add to a uniform base.
+  int roff[MAXK];
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int r = irel[k] < 0 ? 0 : irel[k];
+    roff[k] = 2 * ((r & 255) * ss2 + ((r >> 8) & 255) * ss3 + ((r >> 16) & 255) * ss4);
+  }
   // Activation prefetch depth in stages: two where the registers allow it.
   constexpr int DIST = (NB == 1 || (NB == 2 && WF) || (MODE == MODE_K3 && NB == 3 && !WF)) ? 2 : 1;
   uint4 pfa[DIST][G8 * MAXK];
@@ -210,13 +218,15 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
   // carries so the per-stage index math is a few scalar adds (the divisions
   // happen once per workgroup).
   struct Cursor {
-    int chunk, ct, bw, bh, bd, n;
+    int chunk, split, ct, bw, bh, bd, n;
   };
   auto cursor_at = [&](int job) {
     Cursor c;
-    c.chunk = 0;
-    c.ct = job % a.n_ctiles;
-    int b = job / a.n_ctiles;
+    c.split = job % a.nsplit;
+    c.chunk = c.split * a.cps;
+    const int tile = job / a.nsplit;
+    c.ct = tile % a.n_ctiles;
+    int b = tile / a.n_ctiles;
     c.bw = b % a.nbw;
     b /= a.nbw;
     c.bh = b % a.nbh;
@@ -226,7 +236,9 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
     return c;
   };
   auto advance = [&](Cursor& c) {
-    if (++c.chunk < a.nchunks) return;
+    if (++c.chunk < (c.split + 1) * a.cps) return;
+    if (++c.split < a.nsplit) return;  // chunk is already split * cps
+    c.split = 0;
     c.chunk = 0;
     if (++c.ct < a.n_ctiles) return;
     c.ct = 0;
@@ -260,13 +272,14 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
 #pragma unroll
     for (int cg = 0; cg < G8; ++cg) {
       const int c0 = chunk * 8 * G8 + cg * 8;
+      const int base = 2 * (s0d * ss2 + s0h * ss3 + s0w * ss4 + c0 * ss1);  // uniform
 #pragma unroll
       for (int k = 0; k < MAXK; ++k) {
         const int r = irel[k];
         const int gd = s0d + (r & 255), gh = s0h + ((r >> 8) & 255), gw = s0w + ((r >> 16) & 255);
         const bool ok = r >= 0 && (unsigned)gd < (unsigned)a.Sd && (unsigned)gh < (unsigned)a.Sh &&
                         (unsigned)gw < (unsigned)a.Sw && c0 < a.Cs;
-        const int off = 2 * (gd * ss2 + gh * ss3 + gw * ss4 + c0 * ss1);
+        const int off = base + roff[k];
         if (CL) {
           pfa[slot][cg * MAXK + k] =
               __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, ok ? off : kOob, 0, 0));
@@ -323,75 +336,11 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
 
-  if (WF) {  // every chunk's weights, once (a single column tile: fragments are contiguous)
-    const u32x4_t* wsrc4 = reinterpret_cast<const u32x4_t*>(a.wpk);
-    for (int e = tid; e < a.nchunks * WFRAG; e += 256)
-      *reinterpret_cast<u32x4_t*>(wts + e) = wsrc4[e];
-  }
-  // Stage t walks (job, chunk) from (j0, 0).  Activations are loaded DIST
-  // stages ahead, per-stage weights one stage ahead; `cc` is the stage being
-  // computed, `ca` / `cw` the next activation / weight stage to issue.
-  const int nstage = (j1 - j0) * a.nchunks;
-  Cursor cc = cursor_at(j0);
-  Cursor ca = cc, cw = cc;
-  issue_act(ca, 0);
-  advance(ca);
-  if (!WF) {
-    issue_w(cw);
-    advance(cw);
-  }
-  if (DIST == 2 && nstage > 1) {
-    issue_act(ca, DIST - 1);
-    advance(ca);
-  }
-  // With two slots the loop is unrolled by two so each slot is a fixed set of
-  // registers (no copies of loads still in flight).
-  auto run_stage = [&](int t, auto slot_c) {
-    constexpr int SL = decltype(slot_c)::value;
-    const int chunk = cc.chunk;
-    const int buf = nbuf == 2 ? (t & 1) : 0;
-    commit_act(SL, buf);
-    if (!WF) commit_w(buf);
-    lds_barrier();
-    if (t + DIST < nstage) {
-      issue_act(ca, SL);  // in flight during the next DIST stages
-      advance(ca);
-    }
-    if (!WF && t + 1 < nstage) {
-      issue_w(cw);
-      advance(cw);
-    }
-
-    const int ct = cc.ct;
-    const uint4* wc = WF ? wts + chunk * WFRAG : wts + buf * WFRAG;
-    const uint4* ab = act + buf * ABUF;
-    // Fragments are read PD steps ahead of the MFMAs that use them (two steps
-    // when a step has only MB MFMAs, fewer than an LDS read's latency covers).
-    constexpr int PD = NB == 1 ? 2 : 1;
-    uint4 bfr[PD + 1][NB], afr[PD + 1][MB];
-    auto read_step = [&](int st, int slot) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) bfr[slot][nb] = wc[(st * NB + nb) * 64 + lane];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) afr[slot][mb] = ab[rowbase[mb] + kof[st]];
-    };
-#pragma unroll
-    for (int st = 0; st < PD; ++st)
-      if (st < NSTEP) read_step(st, st);
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-      const int cur = s % (PD + 1);
-      if (s + PD < NSTEP) read_step(s + PD, (s + PD) % (PD + 1));
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr[cur][mb], bfr[cur][nb], acc[mb][nb]);
-    }
-
-    if (chunk == a.nchunks - 1) {
+  // Epilogue of output tile `ec`: acc (+ bias) -> 16-bit -> per-wave scratch
+  // -> 16-byte global stores in the destination's layout.
+  auto epilogue = [&](const Cursor& ec) __attribute__((always_inline)) {
       // Epilogue: lane (g, i) holds rows 8q + 4g + r (w positions) of column i.
-      const int n = cc.n, bd = cc.bd, bh = cc.bh, bw = cc.bw;
+      const int n = ec.n, bd = ec.bd, bh = ec.bh, bw = ec.bw, ct = ec.ct;
       const int r0d = bd * a.TD, r0h = bh * a.TH, r0w = bw * 32;
       const int64_t* sd = a.sd;
       uint16_t* dstn = a.dst + (int64_t)n * sd[0];
@@ -490,11 +439,116 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
             __builtin_amdgcn_wave_barrier();
           }
         }
+      }
+  };
+  // Split K: the tile's partial sums of this split, in lane order
+  // [tile][split][wave][MB*NB*16][64]; the epilogue phase adds the splits.
+  constexpr int PW = MB * NB * 16 * 64;  // floats per wave
+  auto tile_of = [&](const Cursor& c) {
+    return (((c.n * a.nbd + c.bd) * a.nbh + c.bh) * a.nbw + c.bw) * a.n_ctiles + c.ct;
+  };
+  auto store_partial = [&](const Cursor& c) __attribute__((always_inline)) {
+    float* mine = a.part + (((size_t)tile_of(c) * a.nsplit + c.split) * 4 + wv) * PW + lane;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) __builtin_nontemporal_store(acc[mb][nb][e], mine + ((mb * NB + nb) * 16 + e) * 64);
+  };
+  if (a.phase == 1) {
+    // Epilogue phase: one workgroup per output tile, acc = ((0 + p_0) + p_1) + ...
+    // in split order (the same order for every tile and every run).
+    const Cursor ec = cursor_at(blockIdx.x * a.nsplit);
+    const float* pt = a.part + ((size_t)blockIdx.x * a.nsplit * 4 + wv) * PW + lane;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+      const float* ps = pt + (size_t)sp * 4 * PW;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[mb][nb][e] += __builtin_nontemporal_load(ps + ((mb * NB + nb) * 16 + e) * 64);
+    }
+    __syncthreads();  // the bias table is complete
+    epilogue(ec);
+    return;
+  }
+  if (WF) {  // every chunk's weights, once (a single column tile: fragments are contiguous)
+    const u32x4_t* wsrc4 = reinterpret_cast<const u32x4_t*>(a.wpk);
+    for (int e = tid; e < a.nchunks * WFRAG; e += 256)
+      *reinterpret_cast<u32x4_t*>(wts + e) = wsrc4[e];
+  }
+  // Stage t walks (job, chunk) from (j0, first chunk of j0's split).  Activations are loaded DIST
+  // stages ahead, per-stage weights one stage ahead; `cc` is the stage being
+  // computed, `ca` / `cw` the next activation / weight stage to issue.
+  const int nstage = (j1 - j0) * a.cps;
+  Cursor cc = cursor_at(j0);
+  Cursor ca = cc, cw = cc;
+  issue_act(ca, 0);
+  advance(ca);
+  if (!WF) {
+    issue_w(cw);
+    advance(cw);
+  }
+  if (DIST == 2 && nstage > 1) {
+    issue_act(ca, DIST - 1);
+    advance(ca);
+  }
+  // With two slots the loop is unrolled by two so each slot is a fixed set of
+  // registers (no copies of loads still in flight).
+  auto run_stage = [&](int t, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    const int chunk = cc.chunk;
+    const int buf = nbuf == 2 ? (t & 1) : 0;
+    commit_act(SL, buf);
+    if (!WF) commit_w(buf);
+    lds_barrier();
+    if (t + DIST < nstage) {
+      issue_act(ca, SL);  // in flight during the next DIST stages
+      advance(ca);
+    }
+    if (!WF && t + 1 < nstage) {
+      issue_w(cw);
+      advance(cw);
+    }
+
+    const int ct = cc.ct;
+    const uint4* wc = WF ? wts + chunk * WFRAG : wts + buf * WFRAG;
+    const uint4* ab = act + buf * ABUF;
+    // Fragments are read PD steps ahead of the MFMAs that use them (two steps
+    // when a step has only MB MFMAs, fewer than an LDS read's latency covers).
+    constexpr int PD = NB == 1 ? 2 : 1;
+    uint4 bfr[PD + 1][NB], afr[PD + 1][MB];
+    auto read_step = [&](int st, int slot) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bfr[slot][nb] = wc[(st * NB + nb) * 64 + lane];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) afr[slot][mb] = ab[rowbase[mb] + kof[st]];
+    };
+#pragma unroll
+    for (int st = 0; st < PD; ++st)
+      if (st < NSTEP) read_step(st, st);
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      const int cur = s % (PD + 1);
+      if (s + PD < NSTEP) read_step(s + PD, (s + PD) % (PD + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr[cur][mb], bfr[cur][nb], acc[mb][nb]);
+    }
+
+    if (chunk == (cc.split + 1) * a.cps - 1) {
+      if (a.nsplit > 1) store_partial(cc);
+      else epilogue(cc);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
-      }
     }
     if (nbuf == 1 && t + 1 < nstage) lds_barrier();  // the next commit overwrites the buffers
     advance(cc);
@@ -516,7 +570,7 @@ static void launch_row_inst(const RowArgs& a, int cus, size_t lds, hipStream_t s
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 256, lds) != hipSuccess || occ < 1) occ = 1;
   const int64_t cap = (int64_t)cus * occ;
-  const int grid = (int)(a.njobs < cap ? a.njobs : cap);
+  const int grid = a.phase == 1 ? a.ntiles : (int)(a.njobs < cap ? a.njobs : cap);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, stream, a);
 }
 

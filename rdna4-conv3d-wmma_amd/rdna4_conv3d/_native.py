@@ -132,7 +132,7 @@ def device_supported(device_index: int) -> bool:
     return bool(load().r3c_device_supported(int(device_index)))
 
 
-KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout")
+KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout", "split_epilogue")
 
 
 def timing_enable(on: bool) -> None:
