@@ -149,9 +149,14 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
   float* btab = reinterpret_cast<float*>(wts + wslots + 4 * 128);
   const int nbcol = a.nbt_pad * 32;
 
-  // Contiguous job range of this workgroup; a job is (box, column tile).
-  const int j0 = (int)(((int64_t)blockIdx.x * a.njobs) / gridDim.x);
-  const int j1 = (int)(((int64_t)(blockIdx.x + 1) * a.njobs) / gridDim.x);
+  // Contiguous job range of this workgroup; a job is (box, column tile, split).
+  // Workgroups are dealt to the 8 XCDs round-robin (blockIdx % 8); renumbering
+  // them so each XCD owns one contiguous eighth of the jobs keeps boxes that
+  // share tap halos (neighbours in d and h) on the same L2.
+  const int nwg = gridDim.x;
+  const int wg = (a.phase == 0 && (nwg & 7) == 0) ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int j0 = (int)(((int64_t)wg * a.njobs) / nwg);
+  const int j1 = (int)(((int64_t)(wg + 1) * a.njobs) / nwg);
   if (j0 >= j1) return;
 
   // Slot offset of k group 2s + g (tap, channel group) for each step s of this

@@ -65,7 +65,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const int s = lane & 15;          // lane inside its 16-lane group
   const int li = lane & 31;
 
-  int bid = blockIdx.x;
+  // Workgroups are dealt to the 8 XCDs round-robin; renumbering them so each
+  // XCD owns a contiguous eighth keeps boxes whose halos overlap on one L2.
+  const int nwg = gridDim.x;
+  int bid = (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   const int ft = bid % a.n_ftiles;
   bid /= a.n_ftiles;
   const int gt = bid % a.n_gtiles;
