@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
@@ -488,6 +489,10 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   a.src_cl = cl;
   a.part = part;
   a.ntiles = (int32_t)p.ntiles;
+  {
+    const int64_t span = (int64_t)a.ncols * std::llabs(a.sd[1]) + 64 * std::llabs(a.sd[4]) + 64;
+    a.off32 = span < (1ll << 31) ? 1 : 0;
+  }
   a.phase = 0;
   const int64_t jobs = p.ntiles * a.nsplit;
   if (jobs >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");

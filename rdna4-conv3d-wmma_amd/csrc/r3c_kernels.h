@@ -50,6 +50,7 @@ struct RowArgs {
   int32_t nsplit, cps;     // K splits per output tile and chunks per split (nchunks = nsplit * cps)
   float* part;             // nsplit > 1: fp32 partial tiles [tile][split][wave][MB*NB*16][64]
   int32_t ntiles;          // output tiles (box, column tile)
+  int32_t off32;           // 1: epilogue per-lane offsets (columns x c-stride + 32 x w-stride) fit in int32
   int32_t phase;           // 0: main pass; 1: split-K epilogue pass, one workgroup per tile
 };
 

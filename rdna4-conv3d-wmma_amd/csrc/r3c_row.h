@@ -357,6 +357,9 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
         const int td = r / a.TH, th = r - (r / a.TH) * a.TH;
         const int rd = r0d + td, rh = r0h + th;
         if (rd < a.Rd && rh < a.Rh) {
+          // Uniform base of this output line at w = r0w; per-lane offsets are
+          // 32-bit when the host found they fit (off32).
+          uint16_t* lineb = dstn + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + (int64_t)r0w * sd[4];
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const int colbase = (ct * NB + nb) * 32;
@@ -384,7 +387,7 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
                 const int rw = r0w + pc * 8;
                 const uint4 v = *reinterpret_cast<const uint4*>(scr + c * 32 + pc * 8);
                 if (col < a.ncols && rw < a.Rw) {
-                  uint16_t* p = dstn + (int64_t)col * sd[1] + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + rw;
+                  uint16_t* p = lineb + (a.off32 ? (int64_t)(col * (int)sd[1] + pc * 8) : (int64_t)col * sd[1] + pc * 8);
                   if (rw + 8 <= a.Rw && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
                     *reinterpret_cast<uint4*>(p) = v;
                   } else {
@@ -413,7 +416,7 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
                         (int64_t)(2 * rw + kw) * sd[4];
                     nvalid = 8;
                   } else {
-                    p = dstn + (int64_t)col + (int64_t)rd * sd[2] + (int64_t)rh * sd[3] + (int64_t)rw * sd[4];
+                    p = lineb + (a.off32 ? (int64_t)(col + (p0 + sl) * (int)sd[4]) : col + (int64_t)(p0 + sl) * sd[4]);
                     nvalid = a.ncols - col < 8 ? a.ncols - col : 8;
                   }
                   if (nvalid == 8 && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
