@@ -19,44 +19,57 @@ namespace r3c {
 //   T2DX            : ConvTranspose w (Cin, Cout, 8) -> w[col][ci][tap]
 //   T2FWD           : column = tap * Cout + co     -> w[ci][co][tap]
 //                     (_tr_pack_w, conv3d_wmma.py:1453-1455, columns (tap, co))
-__global__ void pack_weight_kernel(const PackArgs a) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.total) return;
-  const int e = (int)(idx & 7);
-  const int lane = (int)((idx >> 3) & 63);
-  int64_t rest = idx >> 9;
-  const int nb = (int)(rest % a.nbt_pad);
+__global__ __launch_bounds__(256) void pack_weight_kernel(const PackArgs a) {
+  // One thread = one lane's 8-element fragment (16 bytes): index v over
+  // [chunk][step][colblock][lane]; 32-bit arithmetic (total < 2^31 elements).
+  const int v = (int)(blockIdx.x * 256 + threadIdx.x);
+  if ((int64_t)v * 8 >= a.total) return;
+  const int lane = v & 63;
+  int rest = v >> 6;
+  const int nb = rest % a.nbt_pad;
   rest /= a.nbt_pad;
-  const int s = (int)(rest % a.nstep);
-  const int chunk = (int)(rest / a.nstep);
+  const int s = rest % a.nstep;
+  const int chunk = rest / a.nstep;
   const int g = lane >> 5, j = lane & 31;
   const int g8 = a.ck / 8;
   const int kg = 2 * s + g;
-  uint16_t v = 0;
-  if (kg < a.taps * g8) {
-    const int tap = kg / g8, cg = kg % g8;
-    const int ci = chunk * a.ck + cg * 8 + e;
-    const int col = nb * 32 + j;
-    if (ci < a.cs && col < a.ncols) {
-      const int mode = a.mode & 15;
-      const bool dx = (a.mode & 16) != 0;
-      if (mode == MODE_K1 || mode == MODE_K3) {
-        if (!dx) v = a.w[((int64_t)col * a.w_cin + ci) * a.taps + tap];
-        else v = a.w[((int64_t)ci * a.w_cin + col) * a.taps + (a.taps - 1 - tap)];
-      } else if (mode == MODE_T2DX) {
-        v = a.w[((int64_t)col * a.w_cout + ci) * 8 + tap];
-      } else if (mode == MODE_T2FWD) {
-        const int t8 = col / a.w_cout, co = col - t8 * a.w_cout;
-        v = a.w[((int64_t)ci * a.w_cout + co) * 8 + t8];
+  const int col = nb * 32 + j;
+  const int mode = a.mode & 15;
+  const bool dx = (a.mode & 16) != 0;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  if (kg < a.taps * g8 && col < a.ncols) {
+    const int tap = kg / g8, cg = kg - (kg / g8) * g8;
+    const int ci0 = chunk * a.ck + cg * 8;
+    // Element e reads w[base + e * estride] (channel ci0 + e).
+    int64_t base, estride;
+    if (mode == MODE_K1 || mode == MODE_K3) {
+      if (!dx) {
+        base = ((int64_t)col * a.w_cin + ci0) * a.taps + tap;
+        estride = a.taps;
+      } else {
+        base = ((int64_t)ci0 * a.w_cin + col) * a.taps + (a.taps - 1 - tap);
+        estride = (int64_t)a.w_cin * a.taps;
       }
+    } else if (mode == MODE_T2DX) {
+      base = ((int64_t)col * a.w_cout + ci0) * 8 + tap;
+      estride = 8;
+    } else {  // MODE_T2FWD
+      const int t8 = col / a.w_cout, co = col - t8 * a.w_cout;
+      base = ((int64_t)ci0 * a.w_cout + co) * 8 + t8;
+      estride = (int64_t)a.w_cout * 8;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = ci0 + e < a.cs ? a.w[base + e * estride] : 0u;
+      w[e >> 1] |= h << (16 * (e & 1));
     }
   }
-  a.out[idx] = v;
+  reinterpret_cast<uint4*>(a.out)[v] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream) {
   (void)dtype;  // a raw 16-bit copy: the element type does not matter
-  const int64_t blocks = (a.total + 255) / 256;
+  const int64_t blocks = (a.total / 8 + 255) / 256;
   hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 

@@ -143,3 +143,47 @@ def test_convt_native_parity(case, layout, dtype):
     assert e_dx <= TOL_DX
     assert e_dw <= TOL_DW
     assert e_db <= TOL_DW
+
+
+# Shapes that take the scheduling branches: split K in the row kernel (fewer
+# output tiles than CUs), the NDHWC copy of a low-channel NCDHW operand, and a
+# many-split weight-gradient reduce (two-level).
+DETERMINISM_CASES = [
+    (1, 192, 192, 4, 8, 16, 3, 1),   # row kernel split K (fwd and dX)
+    (2, 24, 24, 16, 32, 32, 3, 1),   # NCDHW copy path; dW with two-level reduce
+]
+
+
+@requires_gfx950
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("case", DETERMINISM_CASES, ids=lambda c: "n{}c{}-{}_{}x{}x{}_k{}p{}".format(*c))
+def test_native_bitwise_repeatable(case, layout):
+    """Fixed split and fixed-order sums: two runs give identical bits, and the
+    result matches the float64 reference (same tolerances as above)."""
+    nat = _native()
+    n, cin, cout, d, h, w, k, pad = case
+    print(f"case determinism {case} {layout}", flush=True)
+    dtype = torch.bfloat16
+    x = gen((n, cin, d, h, w), 0, dtype)
+    wt = kaiming_weight((cout, cin, k, k, k), cin * k ** 3, 1, dtype)
+    b = gen((cout,), 4, dtype)
+    go = gen((n, cout, d, h, w), 2, dtype)
+    y_ref, dx_ref, dw_ref, db_ref = _ref_conv(x, wt, b, pad, go)
+    xg = to_layout(x.cuda(), layout)
+    gog = to_layout(go.cuda(), layout)
+    wg, bg = wt.cuda(), b.cuda()
+    runs = []
+    for _ in range(2):
+        y = nat.conv3d_fwd(xg, wg, bg, (pad, pad, pad))
+        dx = nat.conv3d_dx(gog, wg, xg.shape, (pad, pad, pad), like=xg)
+        dw, db = nat.conv3d_dw(xg, gog, wg.shape, (pad, pad, pad), torch.float32, want_db=True,
+                               db_dtype=torch.float32)
+        torch.cuda.synchronize()
+        runs.append([t.detach().cpu() for t in (y, dx, dw, db)])
+    for a_, b_ in zip(*runs):
+        assert torch.equal(a_, b_)
+    y, dx, dw, db = runs[0]
+    assert max_rel(y, y_ref) <= TOL_FWD
+    assert max_rel(dx, dx_ref) <= TOL_DX
+    assert max_rel(dw, dw_ref) <= TOL_DW
+    assert max_rel(db, db_ref) <= TOL_DW
