@@ -28,8 +28,8 @@ R3C_DECL_ROW(t2dx)
 R3C_DECL_ROW(t2fwd)
 #undef R3C_DECL_ROW
 #define R3C_DECL_WG(m)                                                                    \
-  bool launch_wgrad_##m##_bf16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s); \
-  bool launch_wgrad_##m##_f16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s);
+  bool launch_wgrad_##m##_bf16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s); \
+  bool launch_wgrad_##m##_f16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s);
 R3C_DECL_WG(k3)
 R3C_DECL_WG(k1)
 R3C_DECL_WG(t2dw)
@@ -51,12 +51,15 @@ bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, i
   }
 }
 
-bool launch_wgrad(int dtype, int mode, int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s) {
+bool launch_wgrad(int dtype, int mode, int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s) {
   const bool bf = dtype == R3C_BF16;
   switch (mode) {
-    case MODE_K3: return bf ? launch_wgrad_k3_bf16(cbw, cl, a, lds, s) : launch_wgrad_k3_f16(cbw, cl, a, lds, s);
-    case MODE_K1: return bf ? launch_wgrad_k1_bf16(cbw, cl, a, lds, s) : launch_wgrad_k1_f16(cbw, cl, a, lds, s);
-    case MODE_T2DW: return bf ? launch_wgrad_t2dw_bf16(cbw, cl, a, lds, s) : launch_wgrad_t2dw_f16(cbw, cl, a, lds, s);
+    case MODE_K3:
+      return bf ? launch_wgrad_k3_bf16(cbw, cl, fl, a, lds, s) : launch_wgrad_k3_f16(cbw, cl, fl, a, lds, s);
+    case MODE_K1:
+      return bf ? launch_wgrad_k1_bf16(cbw, cl, fl, a, lds, s) : launch_wgrad_k1_f16(cbw, cl, fl, a, lds, s);
+    case MODE_T2DW:
+      return bf ? launch_wgrad_t2dw_bf16(cbw, cl, fl, a, lds, s) : launch_wgrad_t2dw_f16(cbw, cl, fl, a, lds, s);
     default: return false;
   }
 }
@@ -520,6 +523,7 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // ---------------------------------------------------------------------------
 struct WgPlan {
   int mode, cbw, taps, ngroups;
+  int fl;  // 1: F staged channel-major from its w-contiguous source
   WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
@@ -553,7 +557,11 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   // ConvTranspose passes stage strided operands directly.
   p.fcopy_bytes = p.gcopy_bytes = 0;
   const bool copy_ok = p.mode == MODE_K3;
-  if (copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
+  // F needs no tap halo: a w-contiguous F (NCDHW) is staged channel-major
+  // straight from the source (fl 1), with no copy.
+  p.fl = (a.fs[4] == 1 && a.Rw % 8 == 0 && a.fs[0] % 8 == 0 && a.fs[1] % 8 == 0 && a.fs[2] % 8 == 0 &&
+          a.fs[3] % 8 == 0) ? 1 : 0;
+  if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
     p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
     channels_last_strides(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
   }
@@ -640,11 +648,15 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   }
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
-  // Channel-contiguous 16-byte staging when both operands allow it, else 8 scalar loads per slot.
-  const int cl = (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0 && vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0) ? 1 : 0;
+  // F channel-major needs a 16-byte aligned source; G (and F when not
+  // channel-major) use 16-byte channel vectors when both allow, else 8 scalar
+  // loads per slot.
+  const int fl = (p.fl && (reinterpret_cast<uintptr_t>(a.fsrc) & 15) == 0) ? 1 : 0;
+  const bool g_ok = vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0;
+  const int cl = (g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0;
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
   TimedLaunch tl(KIND_WGRAD, s);
-  const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, a, p.lds, s);
+  const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, fl, a, p.lds, s);
   tl.end();
   if (!launched) return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d cbw %d", p.mode, p.cbw);
   rc = check_launch("weight-gradient kernel");

@@ -69,9 +69,13 @@ struct WgGeom {
   static constexpr int BOXPOS = LINES * 16;
   static constexpr int HPOS = HD * HH * HW;
   static constexpr int THREADS = 512;                                 // 8 waves
-  static constexpr int NFI = (BOXPOS * 4 + THREADS - 1) / THREADS;   // F staging items (8 channels) per thread
+  static constexpr int NFI = (BOXPOS * 4 + THREADS - 1) / THREADS;   // F staging items (16 bytes) per thread
+  // F tile: [position][32 channels], or [32 channels][FP positions] when F is
+  // staged channel-major (w-contiguous source); FT halves either way.
+  static constexpr int FP = BOXPOS + 8;
+  static constexpr int FT = BOXPOS * 32 > 32 * FP ? BOXPOS * 32 : 32 * FP;
   static constexpr int NGI = (HPOS * 4 + THREADS - 1) / THREADS;     // G staging items per thread at GCW = 32
-  static constexpr int LDS_BYTES = 2 * (BOXPOS + HPOS) * 64;          // double-buffered tiles
+  static constexpr int LDS_BYTES = 2 * (FT + HPOS * 32) * 2;          // double-buffered tiles
 };
 
 struct WgArgs {
@@ -134,7 +138,9 @@ struct LayoutArgs {
 // `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
                 hipStream_t stream);
-bool launch_wgrad(int dtype, int mode, int cbw, int cl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
+// cl: G (and, with fl 0, F) staged by 16-byte channel vectors; fl 1: F staged
+// channel-major from a w-contiguous source.
+bool launch_wgrad(int dtype, int mode, int cbw, int cl, int fl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
 // One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).

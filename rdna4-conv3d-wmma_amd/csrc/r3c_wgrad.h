@@ -43,7 +43,14 @@
 namespace r3c {
 
 
-template <typename T, int MODE, int CBW, int CL>
+// CL: G staged by 16-byte channel vectors (else 8 two-byte loads per slot);
+// with FL 0 the same holds for F, whose tile is [position][channel] and is read
+// with ds_read_tr16_b64.  FL 1: F comes from a w-contiguous source (NCDHW) and
+// is staged channel-major, [channel][FP positions], by 16-byte loads of 8
+// positions; its A fragment (8 consecutive positions of one channel) is then a
+// single ds_read_b128, and the padded pitch (FP = BOXPOS + 8) puts the 16
+// lanes of a group on 16 distinct bank slots.
+template <typename T, int MODE, int CBW, int CL, int FL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void wgrad_kernel(const WgArgs a) {
   extern __shared__ uint4 smem4[];
   using Geo = WgGeom<MODE>;
@@ -53,7 +60,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   constexpr int BOXPOS = Geo::BOXPOS, HPOS = Geo::HPOS;
   constexpr int NFI = Geo::NFI, NGI = Geo::NGI;
   constexpr int NT = Geo::THREADS;
-  constexpr int TILE = (BOXPOS + HPOS) * 32;  // halves per buffer
+  constexpr int FP = Geo::FP, FT = Geo::FT;
+  constexpr int LINES = Geo::LINES;
+  constexpr int TILE = FT + HPOS * 32;  // halves per buffer
   constexpr int NDBG = MODE == MODE_T2DW ? CBW : 1;
   constexpr int WS = MODE == MODE_T2DW ? 2 : 1;  // G positions per F position along each axis
 
@@ -125,10 +134,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
   for (int k = 0; k < NFI; ++k) {
     const int it = k * NT + tid;
-    const int pos = CL ? it >> 2 : it % BOXPOS;
-    const int cg = CL ? it & 3 : it / BOXPOS;
-    const int line = pos >> 4;
-    fcode[k] = it < BOXPOS * 4 ? ((line / TH) | ((line % TH) << 8) | ((pos & 15) << 16) | (cg << 24)) : -1;
+    if (FL == 1) {  // (channel, line, half line): 8 positions of one channel
+      const int half = it & 1, line = (it >> 1) % LINES, ch = (it >> 1) / LINES;
+      fcode[k] = it < 32 * LINES * 2 ? ((line / TH) | ((line % TH) << 8) | ((8 * half) << 16) | (ch << 24)) : -1;
+    } else {
+      const int pos = CL ? it >> 2 : it % BOXPOS;
+      const int cg = CL ? it & 3 : it / BOXPOS;
+      const int line = pos >> 4;
+      fcode[k] = it < BOXPOS * 4 ? ((line / TH) | ((line % TH) << 8) | ((pos & 15) << 16) | (cg << 24)) : -1;
+    }
   }
 #pragma unroll
   for (int k = 0; k < NGI; ++k) {
@@ -179,10 +193,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     for (int k = 0; k < NFI; ++k) {
       const int c = fcode[k];
       const int td = c & 255, th = (c >> 8) & 255, tw = (c >> 16) & 255, cg = c >> 24;
-      const int gd = r0d + td, gh = r0h + th, gw = r0w + tw, c0 = fc0 + cg * 8;
-      const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && c0 < a.Fc;
-      const int off = 2 * (gd * fs2 + gh * fs3 + gw * fs4 + c0 * fs1);
-      pf[k] = load8(fsrc, ok, off, a.Fc - c0, fs1);
+      const int gd = r0d + td, gh = r0h + th, gw = r0w + tw;
+      if (FL == 1) {  // 8 positions gw .. gw+7 of channel fc0 + cg (the planner keeps Rw % 8 == 0)
+        const int ch = fc0 + cg;
+        const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && ch < a.Fc;
+        const int off = 2 * (gd * fs2 + gh * fs3 + gw + ch * fs1);
+        pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, ok ? off : kOob, 0, 0));
+      } else {
+        const int c0 = fc0 + cg * 8;
+        const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && c0 < a.Fc;
+        const int off = 2 * (gd * fs2 + gh * fs3 + gw * fs4 + c0 * fs1);
+        pf[k] = load8(fsrc, ok, off, a.Fc - c0, fs1);
+      }
     }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
@@ -197,13 +219,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   };
   auto commit = [&](int buf) {
     uint16_t* ft = tiles + buf * TILE;
-    uint16_t* gtl = ft + BOXPOS * 32;
+    uint16_t* gtl = ft + FT;
 #pragma unroll
     for (int k = 0; k < NFI; ++k) {
       const int c = fcode[k];
       if (c >= 0) {
         const int pos = ((c & 255) * TH + ((c >> 8) & 255)) * 16 + ((c >> 16) & 255);
-        *reinterpret_cast<u32x4_t*>(ft + pos * 32 + (c >> 24) * 8) = pf[k];
+        if (FL == 1) *reinterpret_cast<u32x4_t*>(ft + (c >> 24) * FP + pos) = pf[k];
+        else *reinterpret_cast<u32x4_t*>(ft + pos * 32 + (c >> 24) * 8) = pf[k];
       }
     }
 #pragma unroll
@@ -236,14 +259,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       if (box + 2 < box_end) issue(box + 2);  // in flight during the K loop
     }
     const uint16_t* ftile = tiles + buf * TILE;
-    const uint16_t* gtile = ftile + BOXPOS * 32;
+    const uint16_t* gtile = ftile + FT;
 
 #pragma unroll
     for (int st = 0; st < Geo::LINES; ++st) {
       const int td = st / TH, th = st % TH;
       const int frow = st * 16 * 32;
       const int grow = ((WS * td) * HH + WS * th) * HW * 32;
-      const uint4 ffr = lds_tr_pair(ftile, fo + frow, fo + frow + 4 * 32);
+      const uint4 ffr = FL == 1 ? *reinterpret_cast<const uint4*>(ftile + li * FP + st * 16 + 8 * g)
+                                : lds_tr_pair(ftile, fo + frow, fo + frow + 4 * 32);
       if (do_dbf) accf = mfma32<T>(ffr, ones, accf);
 #pragma unroll
       for (int q = 0; q < CBW; ++q) {
@@ -294,9 +318,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   }
 }
 
-template <typename T, int MODE, int CBW, int CL>
+template <typename T, int MODE, int CBW, int CL, int FL>
 static void launch_wgrad_inst(const WgArgs& a, size_t lds, hipStream_t stream) {
-  auto kern = wgrad_kernel<T, MODE, CBW, CL>;
+  auto kern = wgrad_kernel<T, MODE, CBW, CL, FL>;
   if (lds > 65536) (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(kern, dim3(a.nblocks), dim3(WgGeom<MODE>::THREADS), lds, stream, a);
 }

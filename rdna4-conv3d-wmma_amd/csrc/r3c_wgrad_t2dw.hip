@@ -3,40 +3,72 @@
 
 namespace r3c {
 
-bool launch_wgrad_t2dw_bf16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s) {
-  if (cbw == 1 && cl == 1) {
-    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 1>(a, lds, s);
+bool launch_wgrad_t2dw_bf16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s) {
+  if (cbw == 1 && cl == 1 && fl == 0) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 1, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 2 && cl == 1) {
-    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 1>(a, lds, s);
+  if (cbw == 2 && cl == 1 && fl == 0) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 1, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 1 && cl == 0) {
-    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 0>(a, lds, s);
+  if (cbw == 1 && cl == 0 && fl == 0) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 0, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 2 && cl == 0) {
-    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 0>(a, lds, s);
+  if (cbw == 2 && cl == 0 && fl == 0) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 0, 0>(a, lds, s);
+    return true;
+  }
+  if (cbw == 1 && cl == 1 && fl == 1) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 1, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 2 && cl == 1 && fl == 1) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 1, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 1 && cl == 0 && fl == 1) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 1, 0, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 2 && cl == 0 && fl == 1) {
+    launch_wgrad_inst<bf16_tag, MODE_T2DW, 2, 0, 1>(a, lds, s);
     return true;
   }
   return false;
 }
-bool launch_wgrad_t2dw_f16(int cbw, int cl, const WgArgs& a, size_t lds, hipStream_t s) {
-  if (cbw == 1 && cl == 1) {
-    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 1>(a, lds, s);
+bool launch_wgrad_t2dw_f16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s) {
+  if (cbw == 1 && cl == 1 && fl == 0) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 1, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 2 && cl == 1) {
-    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 1>(a, lds, s);
+  if (cbw == 2 && cl == 1 && fl == 0) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 1, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 1 && cl == 0) {
-    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 0>(a, lds, s);
+  if (cbw == 1 && cl == 0 && fl == 0) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 0, 0>(a, lds, s);
     return true;
   }
-  if (cbw == 2 && cl == 0) {
-    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 0>(a, lds, s);
+  if (cbw == 2 && cl == 0 && fl == 0) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 0, 0>(a, lds, s);
+    return true;
+  }
+  if (cbw == 1 && cl == 1 && fl == 1) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 1, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 2 && cl == 1 && fl == 1) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 1, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 1 && cl == 0 && fl == 1) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 1, 0, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 2 && cl == 0 && fl == 1) {
+    launch_wgrad_inst<f16_tag, MODE_T2DW, 2, 0, 1>(a, lds, s);
     return true;
   }
   return false;
