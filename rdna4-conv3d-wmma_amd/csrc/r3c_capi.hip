@@ -367,7 +367,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   p.cl = (a.ss[1] == 1 && cs % 8 == 0 && a.ss[0] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 &&
           a.ss[4] % 8 == 0) ? 1 : 0;
   const int taps_k = p.mode == MODE_K3 ? 27 : (p.mode == MODE_T2DX ? 8 : 1);
-  const int g8 = taps_k == 1 ? 2 : 1;
+  const int g8 = taps_k == 1 ? 4 : 1;  // the kernel's RowGeom::G8
   p.ck = 8 * g8;
   const int nbt = cdiv(a.ncols, 32);
   static const int opts[] = {3, 2, 1};

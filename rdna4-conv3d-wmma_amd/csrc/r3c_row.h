@@ -65,9 +65,10 @@ struct RowGeom {
   // needs (K3: 2x4 or 4x2 boxes plus halo; T2DX: boxes of 4 rows, 2x in dY).
   static constexpr int MB = MODE == MODE_T2DX ? 1 : 2;
   static constexpr int MAXHPOS = MODE == MODE_K3 ? 4 * 6 * 34 : (MODE == MODE_T2DX ? 16 * 64 : 8 * 32);
-  // A chunk is G8 8-channel groups: one group per tap when there are taps, two
-  // for the single-tap modes so an MFMA step (two groups) carries no padding.
-  static constexpr int G8 = TAPS == 1 ? 2 : 1;
+  // A chunk is G8 8-channel groups: one group per tap when there are taps; four
+  // (two MFMA steps) for the memory-bound single-tap modes, so each pipeline
+  // stage moves more bytes per barrier.
+  static constexpr int G8 = TAPS == 1 ? 4 : 1;
   static constexpr int NSTEP = (TAPS * G8 + 1) / 2;
   static constexpr int MAXK = (MAXHPOS + 255) / 256;  // staging slots per thread per group
 };
