@@ -53,8 +53,16 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const PackArgs a) {
     } else if (mode == MODE_T2DX) {
       base = ((int64_t)col * a.w_cout + ci0) * 8 + tap;
       estride = 8;
-    } else {  // MODE_T2FWD
-      const int t8 = col / a.w_cout, co = col - t8 * a.w_cout;
+    } else {  // MODE_T2FWD: column (tap, co), or ((kd, kh), co, kw) with kw fastest
+      int t8, co;
+      if (a.t2kw) {
+        const int rest = col >> 1, kdkh = rest / a.w_cout;
+        co = rest - kdkh * a.w_cout;
+        t8 = kdkh * 2 + (col & 1);
+      } else {
+        t8 = col / a.w_cout;
+        co = col - t8 * a.w_cout;
+      }
       base = ((int64_t)ci0 * a.w_cout + co) * 8 + t8;
       estride = (int64_t)a.w_cout * 8;
     }

@@ -430,6 +430,10 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   pk.w_cin = d->cin;
   pk.w_cout = d->cout;
   pk.mode = p.mode | (op == OP_CONV_DX ? 16 : 0);
+  // ConvTranspose into a w-contiguous output orders its columns kw-fastest so
+  // the epilogue can interleave kw pairs into 16-byte stores.
+  a.t2kw = (p.mode == MODE_T2FWD && a.sd[4] == 1) ? 1 : 0;
+  pk.t2kw = a.t2kw;
   pk.total = (int64_t)a.nchunks * nstep * a.nbt_pad * 64 * 8;
   p.wpk_bytes = pk.total * 2;
 

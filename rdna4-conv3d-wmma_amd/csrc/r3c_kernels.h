@@ -51,6 +51,8 @@ struct RowArgs {
   float* part;             // nsplit > 1: fp32 partial tiles [tile][split][wave][MB*NB*16][64]
   int32_t ntiles;          // output tiles (box, column tile)
   int32_t off32;           // 1: epilogue per-lane offsets (columns x c-stride + 32 x w-stride) fit in int32
+  int32_t t2kw;            // T2FWD: 1 = columns ((kd, kh), co, kw) with kw fastest (w-contiguous output),
+                           //        0 = columns (tap, co)
   int32_t phase;           // 0: main pass; 1: split-K epilogue pass, one workgroup per tile
 };
 
@@ -123,6 +125,7 @@ struct PackArgs {
   int32_t nchunks, nstep, nbt_pad;
   int32_t w_cin, w_cout;  // parameter dims of the weight tensor
   int64_t total;
+  int32_t t2kw;           // T2FWD column order, as RowArgs::t2kw
 };
 
 // NCDHW -> NDHWC copy of a fully contiguous tensor (C % 8 == 0, S % 8 == 0,

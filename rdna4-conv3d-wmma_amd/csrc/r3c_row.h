@@ -178,7 +178,8 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
   }
   for (int c = tid; c < nbcol; c += 256) {
     float bv = 0.f;
-    if (a.bias && c < a.ncols) bv = to_f32<T>(a.bias[MODE == MODE_T2FWD ? c % a.cout_t2 : c]);
+    if (a.bias && c < a.ncols)
+      bv = to_f32<T>(a.bias[MODE == MODE_T2FWD ? (a.t2kw ? (c >> 1) : c) % a.cout_t2 : c]);
     btab[c] = bv;
   }
 
@@ -378,7 +379,35 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
             // A wave's LDS operations execute in order, so only the compiler
             // must be kept from reordering the scratch writes and reads.
             __builtin_amdgcn_wave_barrier();
-            if (MODE != MODE_T2FWD && pos_contig) {
+            if (MODE == MODE_T2FWD && pos_contig && a.t2kw) {
+              // ConvTranspose into a w-contiguous output: columns 2j, 2j+1 are
+              // kw = 0, 1 of one (kd, kh, co), so positions w of the pair
+              // interleave into 64 consecutive outputs 2w + kw; a lane builds
+              // 8 of them (4 positions x 2 kw) and stores 16 bytes.
+#pragma unroll
+              for (int rd2 = 0; rd2 < 2; ++rd2) {
+                const int id = rd2 * 64 + lane;
+                const int j = id >> 3, kq = id & 7;
+                const int col = colbase + 2 * j;
+                const int w0 = r0w + 4 * kq;
+                const uint2 e0 = *reinterpret_cast<const uint2*>(scr + (2 * j) * 32 + 4 * kq);
+                const uint2 e1 = *reinterpret_cast<const uint2*>(scr + (2 * j + 1) * 32 + 4 * kq);
+                if (col < a.ncols && w0 < a.Rw) {
+                  const int rest = col >> 1, kdkh = rest / a.cout_t2, co = rest - kdkh * a.cout_t2;
+                  uint16_t* p = dstn + (int64_t)co * sd[1] + (int64_t)(2 * rd + (kdkh >> 1)) * sd[2] +
+                                (int64_t)(2 * rh + (kdkh & 1)) * sd[3] + 2 * w0;
+                  const uint4 v = make_uint4(__builtin_amdgcn_perm(e1.x, e0.x, 0x05040100u),
+                                             __builtin_amdgcn_perm(e1.x, e0.x, 0x07060302u),
+                                             __builtin_amdgcn_perm(e1.y, e0.y, 0x05040100u),
+                                             __builtin_amdgcn_perm(e1.y, e0.y, 0x07060302u));
+                  if (w0 + 4 <= a.Rw && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+                    *reinterpret_cast<uint4*>(p) = v;
+                  } else {
+                    for (int k = 0; k < 8 && w0 + (k >> 1) < a.Rw; ++k) p[k] = u4_elem(v, k);
+                  }
+                }
+              }
+            } else if (MODE != MODE_T2FWD && pos_contig) {
               // 8 consecutive positions of one channel per lane (NCDHW).
 #pragma unroll
               for (int rd2 = 0; rd2 < 2; ++rd2) {
