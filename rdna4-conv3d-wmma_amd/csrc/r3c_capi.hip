@@ -351,6 +351,24 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
       break;
   }
   (void)sc;
+  // An unpadded k=1 pass maps each position to itself, so positions can be
+  // walked in any order.  When source and destination both hold each
+  // channel's D*H*W positions contiguously (NCDHW), view them as [S/256][8][32]:
+  // a box of 8 lines x 32 is then 256 consecutive positions, one 512-byte run
+  // per channel, instead of 8 runs of 64 bytes (w = 32 of a wider row).
+  if (p.mode == MODE_K1 && a.pd == 0 && a.ph == 0 && a.pw == 0) {
+    const int64_t S = (int64_t)sdd * sh * sw;
+    const bool dense = a.ss[4] == 1 && a.ss[3] == sw && a.ss[2] == (int64_t)sh * sw && a.sd[4] == 1 &&
+                       a.sd[3] == a.Rw && a.sd[2] == (int64_t)a.Rh * a.Rw && a.Rd == sdd && a.Rh == sh &&
+                       a.Rw == sw;
+    if (dense && S % 256 == 0 && S / 256 < (1ll << 30)) {
+      a.Rd = sdd = (int)(S / 256);
+      a.Rh = sh = 8;
+      a.Rw = sw = 32;
+      a.ss[2] = a.sd[2] = 256;
+      a.ss[3] = a.sd[3] = 32;
+    }
+  }
   a.Cs = cs;
   a.Sd = sdd; a.Sh = sh; a.Sw = sw;
   // A low-channel NCDHW source of a k=3 pass is copied to NDHWC first: its
@@ -527,7 +545,7 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // ---------------------------------------------------------------------------
 struct WgPlan {
   int mode, cbw, taps, ngroups;
-  int fl;  // 1: F staged channel-major from its w-contiguous source
+  int fl;  // 1: F staged channel-major from its w-contiguous source; 2: G too (k=1, no padding)
   WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
@@ -565,6 +583,27 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   // straight from the source (fl 1), with no copy.
   p.fl = (a.fs[4] == 1 && a.Rw % 8 == 0 && a.fs[0] % 8 == 0 && a.fs[1] % 8 == 0 && a.fs[2] % 8 == 0 &&
           a.fs[3] % 8 == 0) ? 1 : 0;
+  // A k=1 pass without padding has no tap shift: G sits on F's grid and a
+  // w-contiguous G is staged channel-major the same way (fl 2).
+  if (p.fl && p.mode == MODE_K1 && a.pd == 0 && a.ph == 0 && a.pw == 0 && a.gs[4] == 1 && a.Gw % 8 == 0 &&
+      a.gs[0] % 8 == 0 && a.gs[1] % 8 == 0 && a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0)
+    p.fl = 2;
+  // With no tap shift the positions can be walked in any order.  When both
+  // operands hold each channel's D*H*W positions contiguously, view them as
+  // [S/64][4][16]: a box of 4 x 4 x 16 is then 256 consecutive positions, so a
+  // channel's slice of a box is one 512-byte run instead of 16 runs of 32 bytes.
+  if (p.fl == 2) {
+    const int64_t S = (int64_t)a.Rd * a.Rh * a.Rw;
+    const bool dense = a.fs[2] == (int64_t)a.Rh * a.Rw && a.fs[3] == a.Rw && a.gs[2] == a.fs[2] &&
+                       a.gs[3] == a.fs[3] && a.Gd == a.Rd && a.Gh == a.Rh && a.Gw == a.Rw;
+    if (dense && S % 64 == 0 && S / 64 < (1ll << 30)) {
+      a.Rd = a.Gd = (int32_t)(S / 64);
+      a.Rh = a.Gh = 4;
+      a.Rw = a.Gw = 16;
+      a.fs[2] = a.gs[2] = 64;
+      a.fs[3] = a.gs[3] = 16;
+    }
+  }
   if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
     p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
     channels_last_strides(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
@@ -652,12 +691,14 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   }
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
-  // F channel-major needs a 16-byte aligned source; G (and F when not
+  // Channel-major staging needs 16-byte aligned sources; G (and F when not
   // channel-major) use 16-byte channel vectors when both allow, else 8 scalar
   // loads per slot.
-  const int fl = (p.fl && (reinterpret_cast<uintptr_t>(a.fsrc) & 15) == 0) ? 1 : 0;
+  const bool f16b = (reinterpret_cast<uintptr_t>(a.fsrc) & 15) == 0;
+  const bool g16b = (reinterpret_cast<uintptr_t>(a.gsrc) & 15) == 0;
+  const int fl = (p.fl == 2 && f16b && g16b) ? 2 : ((p.fl && f16b) ? 1 : 0);
   const bool g_ok = vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0;
-  const int cl = (g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0;
+  const int cl = fl == 2 ? 1 : ((g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0);
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
   TimedLaunch tl(KIND_WGRAD, s);
   const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, fl, a, p.lds, s);

@@ -77,7 +77,10 @@ struct WgGeom {
   static constexpr int FP = BOXPOS + 8;
   static constexpr int FT = BOXPOS * 32 > 32 * FP ? BOXPOS * 32 : 32 * FP;
   static constexpr int NGI = (HPOS * 4 + THREADS - 1) / THREADS;     // G staging items per thread at GCW = 32
-  static constexpr int LDS_BYTES = 2 * (FT + HPOS * 32) * 2;          // double-buffered tiles
+  // G tile: [position][32 channels], or (k=1 without padding, no tap shift)
+  // channel-major [32 channels][FP positions] like F.
+  static constexpr int GT = HPOS * 32 > 32 * FP ? HPOS * 32 : 32 * FP;
+  static constexpr int LDS_BYTES = 2 * (FT + GT) * 2;                 // double-buffered tiles
 };
 
 struct WgArgs {
@@ -142,7 +145,7 @@ struct LayoutArgs {
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
                 hipStream_t stream);
 // cl: G (and, with fl 0, F) staged by 16-byte channel vectors; fl 1: F staged
-// channel-major from a w-contiguous source.
+// channel-major from a w-contiguous source; fl 2 (k=1, no padding): F and G both.
 bool launch_wgrad(int dtype, int mode, int cbw, int cl, int fl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);

@@ -49,7 +49,8 @@ namespace r3c {
 // is staged channel-major, [channel][FP positions], by 16-byte loads of 8
 // positions; its A fragment (8 consecutive positions of one channel) is then a
 // single ds_read_b128, and the padded pitch (FP = BOXPOS + 8) puts the 16
-// lanes of a group on 16 distinct bank slots.
+// lanes of a group on 16 distinct bank slots.  FL 2 (k=1 without padding,
+// where G has no tap shift): G is staged and read the same way.
 template <typename T, int MODE, int CBW, int CL, int FL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void wgrad_kernel(const WgArgs a) {
   extern __shared__ uint4 smem4[];
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   constexpr int NT = Geo::THREADS;
   constexpr int FP = Geo::FP, FT = Geo::FT;
   constexpr int LINES = Geo::LINES;
-  constexpr int TILE = FT + HPOS * 32;  // halves per buffer
+  constexpr int TILE = FT + Geo::GT;  // halves per buffer
   constexpr int NDBG = MODE == MODE_T2DW ? CBW : 1;
   constexpr int WS = MODE == MODE_T2DW ? 2 : 1;  // G positions per F position along each axis
 
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
   for (int k = 0; k < NFI; ++k) {
     const int it = k * NT + tid;
-    if (FL == 1) {  // (channel, line, half line): 8 positions of one channel
+    if (FL >= 1) {  // (channel, line, half line): 8 positions of one channel
       const int half = it & 1, line = (it >> 1) % LINES, ch = (it >> 1) / LINES;
       fcode[k] = it < 32 * LINES * 2 ? ((line / TH) | ((line % TH) << 8) | ((8 * half) << 16) | (ch << 24)) : -1;
     } else {
@@ -147,6 +148,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
   for (int k = 0; k < NGI; ++k) {
     const int it = k * NT + tid;
+    if (FL == 2) {
+      const int half = it & 1, line = (it >> 1) % LINES, ch = (it >> 1) / LINES;
+      gcode[k] = it < 32 * LINES * 2 ? ((line / TH) | ((line % TH) << 8) | ((8 * half) << 16) | (ch << 24)) : -1;
+      continue;
+    }
     const int hp = CL ? it / ggroups : it % HPOS;
     const int cg = CL ? it - hp * ggroups : it / HPOS;
     const int t = hp / HW;
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       const int c = fcode[k];
       const int td = c & 255, th = (c >> 8) & 255, tw = (c >> 16) & 255, cg = c >> 24;
       const int gd = r0d + td, gh = r0h + th, gw = r0w + tw;
-      if (FL == 1) {  // 8 positions gw .. gw+7 of channel fc0 + cg (the planner keeps Rw % 8 == 0)
+      if (FL >= 1) {  // 8 positions gw .. gw+7 of channel fc0 + cg (the planner keeps Rw % 8 == 0)
         const int ch = fc0 + cg;
         const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && ch < a.Fc;
         const int off = 2 * (gd * fs2 + gh * fs3 + gw + ch * fs1);
@@ -209,6 +215,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
       const int c = gcode[k];
+      if (FL == 2) {  // 8 positions of channel gc0 + ch (k=1 without padding: G sits on the F grid)
+        const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = s0w + ((c >> 16) & 255);
+        const int ch = gc0 + (c >> 24);
+        const bool ok = c >= 0 && gd < a.Gd && gh < a.Gh && gw < a.Gw && ch < a.Gc;
+        const int off = 2 * (gd * gs2 + gh * gs3 + gw + ch * gs1);
+        pg[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, ok ? off : kOob, 0, 0));
+        continue;
+      }
       const int hd = c & 255, hh = (c >> 8) & 255, hw = (c >> 16) & 255, cg = c >> 24;
       const int gd = s0d + hd, gh = s0h + hh, gw = s0w + hw, c0 = gc0 + cg * 8;
       const bool ok = c >= 0 && (unsigned)gd < (unsigned)a.Gd && (unsigned)gh < (unsigned)a.Gh &&
@@ -225,14 +239,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       const int c = fcode[k];
       if (c >= 0) {
         const int pos = ((c & 255) * TH + ((c >> 8) & 255)) * 16 + ((c >> 16) & 255);
-        if (FL == 1) *reinterpret_cast<u32x4_t*>(ft + (c >> 24) * FP + pos) = pf[k];
+        if (FL >= 1) *reinterpret_cast<u32x4_t*>(ft + (c >> 24) * FP + pos) = pf[k];
         else *reinterpret_cast<u32x4_t*>(ft + pos * 32 + (c >> 24) * 8) = pf[k];
       }
     }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
       const int c = gcode[k];
-      if (c >= 0) {
+      if (FL == 2 && c >= 0) {
+        const int pos = ((c & 255) * TH + ((c >> 8) & 255)) * 16 + ((c >> 16) & 255);
+        *reinterpret_cast<u32x4_t*>(gtl + (c >> 24) * FP + pos) = pg[k];
+      } else if (c >= 0) {
         const int hp = ((c & 255) * HH + ((c >> 8) & 255)) * HW + ((c >> 16) & 255);
         *reinterpret_cast<u32x4_t*>(gtl + hp * 32 + (c >> 24) * 8) = pg[k];
       }
@@ -266,13 +283,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       const int td = st / TH, th = st % TH;
       const int frow = st * 16 * 32;
       const int grow = ((WS * td) * HH + WS * th) * HW * 32;
-      const uint4 ffr = FL == 1 ? *reinterpret_cast<const uint4*>(ftile + li * FP + st * 16 + 8 * g)
+      const uint4 ffr = FL >= 1 ? *reinterpret_cast<const uint4*>(ftile + li * FP + st * 16 + 8 * g)
                                 : lds_tr_pair(ftile, fo + frow, fo + frow + 4 * 32);
       if (do_dbf) accf = mfma32<T>(ffr, ones, accf);
 #pragma unroll
       for (int q = 0; q < CBW; ++q) {
         if (!cbok[q]) continue;
-        const uint4 gfr = lds_tr_pair(gtile, go[q] + grow, go[q] + grow + WS * 4 * 32);
+        const uint4 gfr = FL == 2 ? *reinterpret_cast<const uint4*>(gtile + ((q * 8 + wv) * 32 + li) * FP + st * 16 + 8 * g)
+                                  : lds_tr_pair(gtile, go[q] + grow, go[q] + grow + WS * 4 * 32);
         acc[q] = mfma32<T>(ffr, gfr, acc[q]);
         if (MODE == MODE_T2DW) {
           if (do_dbg) accg[q < NDBG ? q : 0] = mfma32<T>(ones, gfr, accg[q < NDBG ? q : 0]);

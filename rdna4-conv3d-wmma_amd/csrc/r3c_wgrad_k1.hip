@@ -20,6 +20,10 @@ bool launch_wgrad_k1_bf16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, 
     launch_wgrad_inst<bf16_tag, MODE_K1, 1, 0, 1>(a, lds, s);
     return true;
   }
+  if (cbw == 1 && cl == 1 && fl == 2) {
+    launch_wgrad_inst<bf16_tag, MODE_K1, 1, 1, 2>(a, lds, s);
+    return true;
+  }
   return false;
 }
 bool launch_wgrad_k1_f16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s) {
@@ -37,6 +41,10 @@ bool launch_wgrad_k1_f16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, h
   }
   if (cbw == 1 && cl == 0 && fl == 1) {
     launch_wgrad_inst<f16_tag, MODE_K1, 1, 0, 1>(a, lds, s);
+    return true;
+  }
+  if (cbw == 1 && cl == 1 && fl == 2) {
+    launch_wgrad_inst<f16_tag, MODE_K1, 1, 1, 2>(a, lds, s);
     return true;
   }
   return false;

@@ -59,6 +59,9 @@ CONV_CASES = [
     (1, 40, 96, 4, 8, 16, 3, 1),
     (1, 96, 40, 4, 8, 20, 3, 1),
     (2, 48, 24, 4, 9, 33, 1, 0),
+    (2, 40, 24, 5, 9, 24, 1, 0),     # k=1 unpadded, w % 8 == 0: both dW operands channel-major in NCDHW
+    (1, 48, 56, 3, 6, 32, 1, 0),
+    (1, 40, 72, 4, 8, 24, 1, 0),     # D*H*W % 256 == 0: flat position order in the k=1 passes
 ]
 
 
