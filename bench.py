@@ -15,12 +15,16 @@ Also reported on the same JSON line:
                 events on its launch stream (the library's timing hook) during the
                 timed steps, against the 2.5 PFLOP/s dense bf16 MFMA peak.
   passes        per-pass kernel time and fraction of peak.
+  hbm_passes    BASELINE configs 3 and 4 (k=1 fp16, ConvTranspose3d k2s2 bf16):
+                per-pass time (all kernels of the pass, median of 20, MALL
+                flushed before each) and compulsory HBM bytes / time vs 8 TB/s.
   cpu_baseline  the reference's CPU path (Conv3dWmma on CPU tensors ->
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
   unet3d        BASELINE config 5: ms per AMP training step (and per sample) of the
                 base=24 UNet3D at batch 4 built with this package's layers, the same
-                with stock nn.Conv3d / nn.ConvTranspose3d, and the largest loss gap.
+                with stock nn.Conv3d / nn.ConvTranspose3d, and the largest loss gap;
+                unet3d_base32 the same at base=32.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
 """
@@ -46,6 +50,11 @@ TRUNK = [  # (N, Cin, Cout, D, H, W)
     (4, 192, 192, 8, 16, 16),
 ]
 PASSES = ("fwd", "dx", "dw")
+# BASELINE configs 3 (pointwise k=1, fp16) and 4 (ConvTranspose3d k=2 s=2, bf16):
+# memory-bound passes, judged on compulsory HBM bytes per pass.
+POINTWISE = [(4, 48, 24, 64, 128, 128), (4, 24, 96, 64, 128, 128)]   # (N, Cin, Cout, D, H, W)
+CONVT = [(4, 192, 96, 8, 16, 16), (4, 48, 24, 32, 64, 64)]           # (N, Cin, Cout, D, H, W) of the input
+FLUSH_BYTES = 512 << 20  # written between repetitions so no pass reads its operands from the 256 MB MALL
 
 
 def _flops(n, ci, co, d, h, w):
@@ -188,6 +197,79 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup):
     return ms, [float(v) for v in losses]
 
 
+def hbm_passes(layout: str, reps: int = 20):
+    """BASELINE configs 3 and 4: per-pass time (median over reps of the summed
+    kernel durations of the pass, HIP events on the launch stream) and the
+    compulsory HBM bytes over that time.  A 512 MB buffer is written before
+    every repetition, so small working sets are not served from the MALL."""
+    import torch
+    from rdna4_conv3d import _native as nat
+    dev = torch.device("cuda", 0)
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+
+    def L(t):
+        return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
+
+    def nbytes(*ts):
+        return sum(t.numel() * t.element_size() for t in ts)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        tot = []
+        for r in range(reps):
+            flush.zero_()
+            nat.timing_enable(True)
+            nat.timing_collect()
+            fn()
+            recs = nat.timing_collect()
+            nat.timing_enable(False)
+            tot.append(sum(ms for _, _, ms in recs))
+        tot.sort()
+        return tot[len(tot) // 2]
+
+    out = {}
+    for (n, ci, co, d, h, w) in POINTWISE:
+        x = L(torch.relu(_gen((n, ci, d, h, w), 0, torch.float16)).to(dev))
+        go = L(_gen((n, co, d, h, w), 2, torch.float16).to(dev))
+        wt = _kaiming((co, ci, 1, 1, 1), ci, 1, torch.float16).to(dev)
+        y = nat.conv3d_fwd(x, wt, None, (0, 0, 0))
+        dw, _ = nat.conv3d_dw(x, go, wt.shape, (0, 0, 0), torch.float32)
+        cases = {
+            "fwd": (lambda: nat.conv3d_fwd(x, wt, None, (0, 0, 0)), nbytes(x, y, wt)),
+            "dx": (lambda: nat.conv3d_dx(go, wt, x.shape, (0, 0, 0), like=x), nbytes(go, x, wt)),
+            "dw": (lambda: nat.conv3d_dw(x, go, wt.shape, (0, 0, 0), torch.float32), nbytes(x, go, dw)),
+        }
+        for p, (fn, by) in cases.items():
+            ms = timed(fn)
+            out[f"k1_{ci}to{co}_{d}x{h}x{w}_fp16_{p}"] = {
+                "us": round(ms * 1e3, 2), "bytes": by, "gbs": round(by / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del x, go, y, dw
+    for (n, ci, co, d, h, w) in CONVT:
+        x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
+        go = L(_gen((n, co, 2 * d, 2 * h, 2 * w), 2, torch.bfloat16).to(dev))
+        wt = _kaiming((ci, co, 2, 2, 2), co * 8, 1, torch.bfloat16).to(dev)
+        b = _kaiming((co,), co * 8, 3, torch.bfloat16).to(dev)
+        y = nat.convt_fwd(x, wt, b)
+        dw, db = nat.convt_dw(x, go, wt.shape, torch.float32, want_db=True, db_dtype=torch.float32)
+        cases = {
+            "fwd": (lambda: nat.convt_fwd(x, wt, b), nbytes(x, y, wt, b)),
+            "dx": (lambda: nat.convt_dx(go, wt, x.shape, like=x), nbytes(go, x, wt)),
+            "dw": (lambda: nat.convt_dw(x, go, wt.shape, torch.float32, want_db=True, db_dtype=torch.float32),
+                   nbytes(x, go, dw, db)),
+        }
+        for p, (fn, by) in cases.items():
+            ms = timed(fn)
+            out[f"convt_{ci}to{co}_{2 * d}x{2 * h}x{2 * w}_bf16_{p}"] = {
+                "us": round(ms * 1e3, 2), "bytes": by, "gbs": round(by / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del x, go, y, dw, db
+    del flush
+    torch.cuda.empty_cache()
+    return out
+
+
 def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     """this package's layers vs stock nn.Conv3d / nn.ConvTranspose3d."""
     import torch
@@ -223,6 +305,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--unet-steps", type=int, default=40, help="UNet3D config-5 timed steps (0 skips it)")
+    ap.add_argument("--no-hbm-passes", action="store_true", help="skip the k=1 / ConvTranspose3d passes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -339,7 +422,9 @@ def main() -> int:
 
     del layers
     torch.cuda.empty_cache()
+    hbm = None if args.no_hbm_passes else hbm_passes(layout)
     unet = unet3d_bench(args.unet_steps, 3) if args.unet_steps > 0 else None
+    unet32 = unet3d_bench(args.unet_steps, 3, base=32) if args.unet_steps > 0 else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -371,7 +456,9 @@ def main() -> int:
         },
         "roofline": roofline,
         "passes": passes,
+        "hbm_passes": hbm,
         "unet3d": unet,
+        "unet3d_base32": unet32,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
