@@ -62,6 +62,9 @@ CONV_CASES = [
     (2, 40, 24, 5, 9, 24, 1, 0),     # k=1 unpadded, w % 8 == 0: both dW operands channel-major in NCDHW
     (1, 48, 56, 3, 6, 32, 1, 0),
     (1, 40, 72, 4, 8, 24, 1, 0),     # D*H*W % 256 == 0: flat position order in the k=1 passes
+    (2, 24, 24, 16, 64, 64, 3, 1),   # more tiles than CUs: multi-job workgroups, no split K
+    (2, 20, 24, 18, 70, 40, 3, 1),   # the same with ragged channels and box edges
+    (2, 1, 24, 16, 64, 64, 3, 1),    # one source channel (the first UNet layer)
 ]
 
 
