@@ -160,6 +160,15 @@ __device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64
     if (a.db_mode == 1) {
 #pragma unroll 8
       for (int s = s0; s < s1; ++s) sum += a.dbpart[(size_t)s * a.Fpad + c];
+    } else if (a.taps == 8) {  // ConvTranspose: the 8 tap partials of a split, loads issued together
+#pragma unroll 4
+      for (int s = s0; s < s1; ++s) {
+        const float* q = a.dbpart + (size_t)s * 8 * a.Gpad + c;
+        float t = 0.f;
+#pragma unroll
+        for (int tap = 0; tap < 8; ++tap) t += q[(size_t)tap * a.Gpad];
+        sum += t;
+      }
     } else {
       for (int s = s0; s < s1; ++s) {
         float t = 0.f;
