@@ -384,6 +384,12 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   // others by 8 scalar loads per slot through registers.
   p.cl = (a.ss[1] == 1 && cs % 8 == 0 && a.ss[0] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 &&
           a.ss[4] % 8 == 0) ? 1 : 0;
+  // A w-contiguous source of a single-tap pass (k=1 without w padding, or
+  // ConvTranspose forward) is staged channel-major by 16-byte loads of 8
+  // positions (cl 2) instead of 8 scalar loads per slot.
+  if (!p.cl && (p.mode == MODE_T2FWD || (p.mode == MODE_K1 && a.pw == 0)) && a.ss[4] == 1 && sw % 8 == 0 &&
+      a.ss[0] % 8 == 0 && a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0)
+    p.cl = 2;
   const int taps_k = p.mode == MODE_K3 ? 27 : (p.mode == MODE_T2DX ? 8 : 1);
   const int g8 = taps_k == 1 ? 4 : 1;  // the kernel's RowGeom::G8
   p.ck = 8 * g8;
@@ -409,6 +415,9 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   }
   const int hpos = a.HD * a.HH * hw;
   a.CGS = (hpos + 15) / 16 * 16;  // 256-byte aligned channel-group planes
+  // Channel-major rows: a pitch of 32 (mod 128) halves puts the rows a
+  // transposing read touches on distinct banks.
+  if (p.cl == 2) a.CGS = (hpos + 127) / 128 * 128 + 32;
   const int taps = taps_k;
   const int nstep = cdiv(taps * g8, 2);
   const int64_t wchunk = (int64_t)nstep * p.nb * 1024;  // bytes of one chunk's fragments

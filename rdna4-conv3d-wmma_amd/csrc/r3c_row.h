@@ -22,6 +22,13 @@
 // read consecutive slots as well.  B fragments are 16-byte loads of the weight
 // pre-packed in lane order.
 //
+// CL 2 (single-tap modes, w-contiguous source, NCDHW): the chunk's 32 channels
+// are staged channel-major, [channel][CGS halves], each thread moving 8
+// consecutive positions of one channel with one 16-byte load; an A fragment is
+// then two ds_read_b64_tr_b16 (4 channels at 16 consecutive positions per
+// 16-lane group each).  CGS = 32 (mod 128) keeps the 16-lane groups of a read
+// on distinct banks.
+//
 // Loads go through a buffer resource with 32-bit offsets: out-of-range
 // positions (the zero padding) use an offset past num_records, which the
 // hardware returns as zero, so there are no bounds branches.
@@ -132,6 +139,8 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
   constexpr int WFRAG = NSTEP * NB * 64;              // uint4 per chunk of weights
   constexpr int WIT = WF ? 1 : (WFRAG + 255) / 256;   // weight uint4 per thread per chunk
 
+  constexpr bool CM = CL == 2;  // channel-major staging
+  static_assert(!CM || (TAPS == 1 && G8 == 4 && MAXK == 1), "channel-major staging: single-tap modes");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -216,6 +225,32 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
     const int r = irel[k] < 0 ? 0 : irel[k];
     roff[k] = 2 * ((r & 255) * ss2 + ((r >> 8) & 255) * ss3 + ((r >> 16) & 255) * ss4);
   }
+  // CM: staging item k*256 + tid = (channel ci, 8-position chunk) of the tile,
+  // coded (hd, hh, hw, ci) 8 bits each; byte offset relative to the tile origin.
+  int cmi[CM ? 4 : 1], cmoff[CM ? 4 : 1];
+  if (CM) {
+    const int nchk = HPOS >> 3;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int it = k * 256 + tid;
+      const int ci = it / nchk, pos = (it - ci * nchk) * 8;
+      const int t = pos / HW, hw = pos - t * HW;
+      const int hd = t / HH, hh = t - hd * HH;
+      cmi[k] = ci < 32 ? (hd | (hh << 8) | (hw << 16) | (ci << 24)) : -1;
+      cmoff[k] = ci < 32 ? 2 * (ci * ss1 + hd * ss2 + hh * ss3 + hw) : 0;
+    }
+  }
+  // CM: this lane's A-fragment half offset for row block mb at step 0
+  // (channel 8g + (lane & 15) / 4, position line start + 16 ((lane >> 4) & 1) + 4 (lane & 3)).
+  int cmrow[CM ? MB : 1];
+  if (CM) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int r = wv * MB + mb;
+      const int td = r / a.TH, th = r - (r / a.TH) * a.TH;
+      cmrow[mb] = (8 * g + ((lane & 15) >> 2)) * HPAD + (td * HH + th) * HW + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    }
+  }
   // Activation prefetch depth in stages: two where the registers allow it.
   constexpr int DIST = (NB == 1 || (NB == 2 && WF) || (MODE == MODE_K3 && NB == 3 && !WF)) ? 2 : 1;
   uint4 pfa[DIST][G8 * MAXK];
@@ -276,6 +311,19 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
       s0w = bw * 32;
     }
     const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (int64_t)n * a.ss[0], a.src_bytes);
+    if (CM) {  // 8 positions of one channel per item (the host keeps Sw % 8 == 0 and s0w >= 0)
+      const int c0 = chunk * 32;
+      const int base = 2 * (s0d * ss2 + s0h * ss3 + s0w + c0 * ss1);  // uniform
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = cmi[k];
+        const int gd = s0d + (r & 255), gh = s0h + ((r >> 8) & 255), gw = s0w + ((r >> 16) & 255);
+        const bool ok = r >= 0 && (unsigned)gd < (unsigned)a.Sd && (unsigned)gh < (unsigned)a.Sh && gw < a.Sw &&
+                        c0 + (r >> 24) < a.Cs;
+        pfa[slot][k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, ok ? base + cmoff[k] : kOob, 0, 0));
+      }
+      return;
+    }
 #pragma unroll
     for (int cg = 0; cg < G8; ++cg) {
       const int c0 = chunk * 8 * G8 + cg * 8;
@@ -321,6 +369,18 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
     }
   };
   auto commit_act = [&](int slot, int buf) {
+    if (CM) {
+      uint16_t* ah = reinterpret_cast<uint16_t*>(act + buf * ABUF);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = cmi[k];
+        if (r >= 0) {
+          const int pos = (((r & 255) * HH + ((r >> 8) & 255)) * HW) + ((r >> 16) & 255);
+          *reinterpret_cast<u32x4_t*>(ah + (r >> 24) * HPAD + pos) = __builtin_bit_cast(u32x4_t, pfa[slot][k]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int cg = 0; cg < G8; ++cg)
 #pragma unroll
@@ -561,8 +621,15 @@ __attribute__((amdgpu_waves_per_eu((MODE == MODE_K3 && NB == 3 && !WF) ? 1 : 2, 
     auto read_step = [&](int st, int slot) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) bfr[slot][nb] = wc[(st * NB + nb) * 64 + lane];
+      if (CM) {
+        const uint16_t* ah = reinterpret_cast<const uint16_t*>(ab);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) afr[slot][mb] = ab[rowbase[mb] + kof[st]];
+        for (int mb = 0; mb < MB; ++mb)
+          afr[slot][mb] = lds_tr_pair(ah, cmrow[mb] + st * 16 * HPAD, cmrow[mb] + st * 16 * HPAD + 4 * HPAD);
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) afr[slot][mb] = ab[rowbase[mb] + kof[st]];
+      }
     };
 #pragma unroll
     for (int st = 0; st < PD; ++st)

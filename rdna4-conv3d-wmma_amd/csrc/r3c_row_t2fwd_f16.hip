@@ -4,6 +4,30 @@
 namespace r3c {
 
 bool launch_row_t2fwd_f16(int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s) {
+  if (wf == 1 && cl == 2 && nb == 1) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 1, 2, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 1 && cl == 2 && nb == 2) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 2, 2, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 1 && cl == 2 && nb == 3) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 3, 2, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 2 && nb == 1) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 1, 2, 0>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 2 && nb == 2) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 2, 2, 0>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 2 && nb == 3) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 3, 2, 0>(a, cus, lds, s);
+    return true;
+  }
   if (wf == 1 && cl == 1 && nb == 1) {
     launch_row_inst<f16_tag, MODE_T2FWD, 1, 1, 1>(a, cus, lds, s);
     return true;

@@ -111,6 +111,7 @@ CONVT_CASES = [
     (1, 48, 24, 4, 8, 16),
     (1, 192, 96, 2, 4, 16),
     (1, 5, 3, 2, 2, 3),
+    (2, 40, 24, 3, 5, 40),   # w % 8 == 0 with a ragged second line and a ragged channel chunk (NCDHW: channel-major staging)
 ]
 
 
