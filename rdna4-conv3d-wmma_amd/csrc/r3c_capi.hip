@@ -27,6 +27,37 @@ R3C_DECL_ROW(k1)
 R3C_DECL_ROW(t2dx)
 R3C_DECL_ROW(t2fwd)
 #undef R3C_DECL_ROW
+#define R3C_DECL_TAP(t)                                                                                     \
+  bool launch_tap_##t(int nb, int mb, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s);
+R3C_DECL_TAP(bf16_w32_s0)
+R3C_DECL_TAP(bf16_w32_s1)
+R3C_DECL_TAP(bf16_w16_s0)
+R3C_DECL_TAP(bf16_w16_s1)
+R3C_DECL_TAP(f16_w32_s0)
+R3C_DECL_TAP(f16_w32_s1)
+R3C_DECL_TAP(f16_w16_s0)
+R3C_DECL_TAP(f16_w16_s1)
+R3C_DECL_TAP(bf16_w32_s3)
+R3C_DECL_TAP(bf16_w16_s3)
+R3C_DECL_TAP(f16_w32_s3)
+R3C_DECL_TAP(f16_w16_s3)
+#undef R3C_DECL_TAP
+
+bool launch_tap(int dtype, int nb, int mb, int src, int wf, int lw, const RowArgs& a, int cus, size_t lds,
+                hipStream_t s) {
+  const bool bf = dtype == R3C_BF16;
+  if (src == 3) {
+    if (lw == 32) return bf ? launch_tap_bf16_w32_s3(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w32_s3(nb, mb, wf, a, cus, lds, s);
+    return bf ? launch_tap_bf16_w16_s3(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w16_s3(nb, mb, wf, a, cus, lds, s);
+  }
+  if (lw == 32) {
+    if (src == 1) return bf ? launch_tap_bf16_w32_s1(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w32_s1(nb, mb, wf, a, cus, lds, s);
+    return bf ? launch_tap_bf16_w32_s0(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w32_s0(nb, mb, wf, a, cus, lds, s);
+  }
+  if (src == 1) return bf ? launch_tap_bf16_w16_s1(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w16_s1(nb, mb, wf, a, cus, lds, s);
+  return bf ? launch_tap_bf16_w16_s0(nb, mb, wf, a, cus, lds, s) : launch_tap_f16_w16_s0(nb, mb, wf, a, cus, lds, s);
+}
+
 #define R3C_DECL_WG(m)                                                                    \
   bool launch_wgrad_##m##_bf16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s); \
   bool launch_wgrad_##m##_f16(int cbw, int cl, int fl, const WgArgs& a, size_t lds, hipStream_t s);
@@ -271,6 +302,8 @@ uint32_t sample_bytes(const int64_t* st, int c, int d, int h, int w) {
 // ---------------------------------------------------------------------------
 struct RowPlan {
   int mode, ck, nb, cl;
+  int tap;             // 1: Conv3d k=3 through the tap kernel (mb, lw below)
+  int mb, lw;
   RowArgs a;
   PackArgs pk;
   size_t lds;
@@ -308,6 +341,107 @@ void pick_box(int rows, int Rd, int Rh, int halo, int td_min, int td_max, int& T
       TH = th;
     }
   }
+}
+
+// Weight packing into the kernel's fragment order ([chunk][step][colblock][lane][8]).
+void plan_pack(const r3c_conv_desc* d, int op, RowPlan& p, int taps, int nstep) {
+  RowArgs& a = p.a;
+  PackArgs& pk = p.pk;
+  memset(&pk, 0, sizeof pk);
+  pk.cs = a.Cs;
+  pk.ncols = a.ncols;
+  pk.taps = taps;
+  pk.ck = p.ck;
+  pk.nchunks = a.nchunks;
+  pk.nstep = nstep;
+  pk.nbt_pad = a.nbt_pad;
+  pk.w_cin = d->cin;
+  pk.w_cout = d->cout;
+  pk.mode = p.mode | (op == OP_CONV_DX ? 16 : 0);
+  // ConvTranspose into a w-contiguous output orders its columns kw-fastest so
+  // the epilogue can interleave kw pairs into 16-byte stores.
+  a.t2kw = (p.mode == MODE_T2FWD && a.sd[4] == 1) ? 1 : 0;
+  pk.t2kw = a.t2kw;
+  pk.total = (int64_t)a.nchunks * nstep * a.nbt_pad * 64 * 8;
+  p.wpk_bytes = pk.total * 2;
+}
+
+// Tap-kernel geometry (mirrors TapGeom in r3c_tap.h): TD x TH lines of `lw`
+// positions (a line spans 32 / lw h rows), a one-voxel halo on every side.
+struct TapBox {
+  int TD, TH, HR, HD, HH, HW, HPOS, HPAD;
+};
+TapBox tap_box(int mb, int lw) {
+  TapBox b;
+  b.TD = mb == 1 ? 2 : 4;
+  b.TH = mb == 4 ? 8 : 4;
+  b.HR = 32 / lw;
+  b.HD = b.TD + 2;
+  b.HH = b.TH * b.HR + 2;
+  b.HW = lw + 2;
+  b.HPOS = b.HD * b.HH * b.HW;
+  b.HPAD = (b.HPOS + 15) / 16 * 16;
+  return b;
+}
+constexpr int64_t kTapScratch = 8 * 32 * 40 * 2;  // epilogue scratch of the 8 waves
+constexpr int kTapStep = 14;                      // MFMA steps per 8-channel chunk (27 taps)
+
+// Conv3d k=3 plan on the tap kernel; `a` already holds the source/destination
+// geometry, strides, padding and channel counts.
+void plan_tap(const r3c_conv_desc* d, RowPlan& p) {
+  RowArgs& a = p.a;
+  p.tap = 1;
+  p.ck = 8;
+  p.lw = a.Rw <= 16 ? 16 : 32;
+  const int nbt = cdiv(a.ncols, 32);
+  static const int opts[] = {3, 2, 1};
+  p.nb = pick_blocks(nbt, opts, 3);
+  a.n_ctiles = cdiv(nbt, p.nb);
+  a.nbt_pad = a.n_ctiles * p.nb;
+  a.nchunks = cdiv(a.Cs, 8);
+  const int64_t wfrag = (int64_t)kTapStep * p.nb * 64 * 16;  // bytes of one chunk's fragments
+  const int64_t fixed = kTapScratch + (int64_t)a.nbt_pad * 32 * 4;
+  // Largest row block per wave (MB lines) that still gives every CU a tile
+  // and fits the LDS; MB = 4 only for a single column block.
+  static const int mbs[] = {4, 2, 1};
+  int chosen = -1;
+  for (int mb : mbs) {
+    if (mb == 4 && p.nb != 1) continue;
+    const TapBox b = tap_box(mb, p.lw);
+    const int64_t tiles = (int64_t)d->n * cdiv(a.Rd, b.TD) * cdiv(a.Rh, b.TH * b.HR) * cdiv(a.Rw, p.lw) * a.n_ctiles;
+    const int64_t lds = fixed + 2 * (int64_t)b.HPAD * 16 + 2 * wfrag;
+    if (lds > kMaxLds) continue;
+    chosen = mb;
+    if (tiles >= kNumCUs) break;
+  }
+  if (chosen < 0) chosen = 1;
+  p.mb = chosen;
+  const TapBox b = tap_box(p.mb, p.lw);
+  a.TD = b.TD;
+  a.TH = b.TH;
+  a.HD = b.HD;
+  a.HH = b.HH;
+  a.CGS = b.HPAD;
+  a.nbd = cdiv(a.Rd, b.TD);
+  a.nbh = cdiv(a.Rh, b.TH * b.HR);
+  a.nbw = cdiv(a.Rw, p.lw);
+  const int64_t act = 2 * (int64_t)b.HPAD * 16;
+  a.wfull = (p.nb == 1 && a.n_ctiles == 1 && fixed + act + wfrag * a.nchunks <= kMaxLds) ? 1 : 0;
+  a.nbuf = 2;
+  p.lds = (size_t)(fixed + act + (a.wfull ? wfrag * a.nchunks : 2 * wfrag));
+  // Deterministic split K over the source-channel chunks when there are fewer
+  // output tiles than CUs: the largest divisor of nchunks with at most one
+  // job per CU.
+  p.ntiles = (int64_t)d->n * a.nbd * a.nbh * a.nbw * a.n_ctiles;
+  int split = 1;
+  if (p.ntiles < kNumCUs) {
+    const int64_t want = kNumCUs / p.ntiles;
+    for (int sp = 2; sp <= a.nchunks && sp <= want; ++sp)
+      if (a.nchunks % sp == 0) split = sp;
+  }
+  a.nsplit = split;
+  a.cps = a.nchunks / split;
+  p.part_bytes = split > 1 ? align256(p.ntiles * split * 8 * p.mb * p.nb * 16 * 64 * 4) : 0;
 }
 
 void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
@@ -375,7 +509,11 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   // channel-contiguous staging is faster than strided staging by more than the
   // copy costs (two bytes read and written per element).
   p.copy_bytes = 0;
-  if (p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
+  // A w-contiguous k=3 source (NCDHW) is staged by 16-byte loads of 8
+  // positions per channel and a register transpose (tap kernel staging mode 3).
+  const bool k3_wvec = p.mode == MODE_K3 && a.ss[4] == 1 && a.ss[1] != 1 && sw % 8 == 0 && a.ss[0] % 8 == 0 &&
+                       a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 && a.pw >= -6 && a.pw <= 8;
+  if (!k3_wvec && p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
     p.copy_bytes = align256(tensor_bytes(d->n, cs, sdd, sh, sw));
     channels_last_strides(a.ss, cs, sdd, sh, sw);
   }
@@ -390,6 +528,15 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   if (!p.cl && (p.mode == MODE_T2FWD || (p.mode == MODE_K1 && a.pw == 0)) && a.ss[4] == 1 && sw % 8 == 0 &&
       a.ss[0] % 8 == 0 && a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0)
     p.cl = 2;
+  if (k3_wvec) p.cl = 3;
+  p.tap = 0;
+  p.mb = 2;
+  p.lw = 32;
+  if (p.mode == MODE_K3) {
+    plan_tap(d, p);
+    plan_pack(d, op, p, 27, kTapStep);
+    return;
+  }
   const int taps_k = p.mode == MODE_K3 ? 27 : (p.mode == MODE_T2DX ? 8 : 1);
   const int g8 = taps_k == 1 ? 4 : 1;  // the kernel's RowGeom::G8
   p.ck = 8 * g8;
@@ -445,24 +592,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   a.wfull = opts2[best].wfull;
   a.nbuf = opts2[best].nbuf;
   p.lds = (size_t)best_lds;
-  PackArgs& pk = p.pk;
-  memset(&pk, 0, sizeof pk);
-  pk.cs = cs;
-  pk.ncols = a.ncols;
-  pk.taps = taps;
-  pk.ck = p.ck;
-  pk.nchunks = a.nchunks;
-  pk.nstep = nstep;
-  pk.nbt_pad = a.nbt_pad;
-  pk.w_cin = d->cin;
-  pk.w_cout = d->cout;
-  pk.mode = p.mode | (op == OP_CONV_DX ? 16 : 0);
-  // ConvTranspose into a w-contiguous output orders its columns kw-fastest so
-  // the epilogue can interleave kw pairs into 16-byte stores.
-  a.t2kw = (p.mode == MODE_T2FWD && a.sd[4] == 1) ? 1 : 0;
-  pk.t2kw = a.t2kw;
-  pk.total = (int64_t)a.nchunks * nstep * a.nbt_pad * 64 * 8;
-  p.wpk_bytes = pk.total * 2;
+  plan_pack(d, op, p, taps, nstep);
 
   // Split K over the source-channel chunks when there are fewer output tiles
   // than CUs: the largest divisor of nchunks that keeps jobs <= kSplitTarget
@@ -534,7 +664,8 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   // The launcher sizes the grid to the resident capacity (CUs x workgroups
   // per CU from the occupancy query); workgroups take contiguous job ranges.
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
+  const bool launched = p.tap ? launch_tap(d->dtype, p.nb, p.mb, cl, a.wfull, p.lw, a, t_cus, p.lds, s)
+                              : launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
   tl.end();
   if (!launched)
     return fail(R3C_UNSUPPORTED, "no row-kernel instantiation for mode %d ck %d nb %d cl %d", p.mode, p.ck, p.nb,
@@ -544,7 +675,8 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   // Split K: the epilogue pass adds each tile's split partial sums in split order.
   a.phase = 1;
   TimedLaunch te(KIND_SPLIT_EPI, s);
-  launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
+  if (p.tap) launch_tap(d->dtype, p.nb, p.mb, cl, a.wfull, p.lw, a, t_cus, p.lds, s);
+  else launch_row(d->dtype, p.mode, p.nb, cl, a.wfull, a, t_cus, p.lds, s);
   te.end();
   return check_launch("row kernel epilogue pass");
 }

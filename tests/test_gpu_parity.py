@@ -194,3 +194,41 @@ def test_native_bitwise_repeatable(case, layout):
     assert max_rel(dx, dx_ref) <= TOL_DX
     assert max_rel(dw, dw_ref) <= TOL_DW
     assert max_rel(db, db_ref) <= TOL_DW
+
+
+# Shapes large enough to reach the k=3 kernel's biggest boxes (32 lines of 32
+# per workgroup, resident or per-stage weights) and its 16-wide-line mode with
+# split K; the reference is torch's own fp32 convolution on the GPU from the
+# same rounded inputs (the float64 CPU path would take minutes here).
+K3_LARGE_CASES = [
+    # (n, cin, cout, d, h, w)
+    (2, 24, 24, 16, 128, 64),    # one column block, 32-line boxes, all weights resident
+    (1, 200, 16, 16, 128, 128),  # one column block, 32-line boxes, per-stage weights (25 chunks)
+    (1, 48, 48, 16, 128, 64),    # two column blocks, 16-line boxes
+    (1, 96, 96, 16, 64, 64),     # three column blocks, 8-line boxes
+    (4, 192, 192, 8, 16, 16),    # 16-wide lines, two column tiles, split K
+]
+
+
+@requires_gfx950
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("case", K3_LARGE_CASES, ids=lambda c: "n{}c{}-{}_{}x{}x{}".format(*c))
+def test_conv3d_k3_large_fwd_dx(case, layout):
+    nat = _native()
+    n, cin, cout, d, h, w = case
+    print(f"case k3 large {case} {layout}", flush=True)
+    dtype = torch.bfloat16
+    x = gen((n, cin, d, h, w), 0, dtype).cuda()
+    wt = kaiming_weight((cout, cin, 3, 3, 3), cin * 27, 1, dtype).cuda()
+    b = gen((cout,), 4, dtype).cuda()
+    go = gen((n, cout, d, h, w), 2, dtype).cuda()
+    y_ref = F.conv3d(x.float(), wt.float(), b.float(), 1, 1)
+    dx_ref = torch.nn.grad.conv3d_input(x.shape, wt.float(), go.float(), 1, 1)
+    xg, gog = to_layout(x, layout), to_layout(go, layout)
+    y = nat.conv3d_fwd(xg, wt, b, (1, 1, 1))
+    dx = nat.conv3d_dx(gog, wt, xg.shape, (1, 1, 1), like=xg)
+    torch.cuda.synchronize()
+    e_y, e_dx = max_rel(y, y_ref), max_rel(dx, dx_ref)
+    print(f"  maxrel y {e_y:.2e} dx {e_dx:.2e}", flush=True)
+    assert e_y <= TOL_FWD
+    assert e_dx <= TOL_DX
