@@ -22,7 +22,6 @@ namespace r3c {
 #define R3C_DECL_ROW(m)                                                                       \
   bool launch_row_##m##_bf16(int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s); \
   bool launch_row_##m##_f16(int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s);
-R3C_DECL_ROW(k3)
 R3C_DECL_ROW(k1)
 R3C_DECL_ROW(t2dx)
 R3C_DECL_ROW(t2fwd)
@@ -69,8 +68,6 @@ R3C_DECL_WG(t2dw)
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds, hipStream_t s) {
   const bool bf = dtype == R3C_BF16;
   switch (mode) {
-    case MODE_K3:
-      return bf ? launch_row_k3_bf16(nb, cl, wf, a, cus, lds, s) : launch_row_k3_f16(nb, cl, wf, a, cus, lds, s);
     case MODE_K1:
       return bf ? launch_row_k1_bf16(nb, cl, wf, a, cus, lds, s) : launch_row_k1_f16(nb, cl, wf, a, cus, lds, s);
     case MODE_T2DX:

@@ -38,7 +38,7 @@
 // [split][Fpad][TAPS][Gpad]; the reduce kernels add the splits in a fixed
 // order.
 #pragma once
-#include "r3c_row.h"
+#include "r3c_tap.h"
 
 namespace r3c {
 
@@ -174,15 +174,72 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     }
     return v;
   };
-  auto issue = [&](int box) {
-    int b = box;
-    const int bw = b % a.nbw;
-    b /= a.nbw;
-    const int bh = b % a.nbh;
-    b /= a.nbh;
-    const int bd = b % a.nbd;
-    const int n = b / a.nbd;
-    const int r0d = bd * Geo::TD, r0h = bh * TH, r0w = bw * 16;
+  // Per-item relative byte offsets inside a box (F) or its halo tile (G),
+  // whether the item exists with its channels in range (fixed per workgroup),
+  // and the channel count left for the element-wise path.
+  int frel[NFI], grel[NGI], fcv[NFI], gcv[NGI];
+  bool fval[NFI], gval[NGI];
+#pragma unroll
+  for (int k = 0; k < NFI; ++k) {
+    const int c = fcode[k];
+    const int td = c & 255, th = (c >> 8) & 255, tw = (c >> 16) & 255, cg = c >> 24;
+    if (FL >= 1) {
+      const int ch = fc0 + cg;
+      frel[k] = 2 * (td * fs2 + th * fs3 + tw + ch * fs1);
+      fval[k] = c >= 0 && ch < a.Fc;
+      fcv[k] = 8;
+    } else {
+      const int c0 = fc0 + cg * 8;
+      frel[k] = 2 * (td * fs2 + th * fs3 + tw * fs4 + c0 * fs1);
+      fval[k] = c >= 0 && c0 < a.Fc;
+      fcv[k] = a.Fc - c0;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NGI; ++k) {
+    const int c = gcode[k];
+    const int hd = c & 255, hh = (c >> 8) & 255, hw = (c >> 16) & 255, cg = c >> 24;
+    if (FL == 2) {
+      const int ch = gc0 + cg;
+      grel[k] = 2 * (hd * gs2 + hh * gs3 + hw + ch * gs1);
+      gval[k] = c >= 0 && ch < a.Gc;
+      gcv[k] = 8;
+    } else {
+      const int c0 = gc0 + cg * 8;
+      grel[k] = 2 * (hd * gs2 + hh * gs3 + hw * gs4 + c0 * gs1);
+      gval[k] = c >= 0 && c0 < a.Gc;
+      gcv[k] = a.Gc - c0;
+    }
+  }
+
+  // Box cursor (w fastest), advanced by carries: the divisions happen once.
+  struct BoxCur {
+    int bw, bh, bd, n;
+  };
+  auto box_at = [&](int box) {
+    BoxCur c;
+    c.bw = box % a.nbw;
+    box /= a.nbw;
+    c.bh = box % a.nbh;
+    box /= a.nbh;
+    c.bd = box % a.nbd;
+    c.n = box / a.nbd;
+    return c;
+  };
+  auto box_advance = [&](BoxCur& c) {
+    if (++c.bw < a.nbw) return;
+    c.bw = 0;
+    if (++c.bh < a.nbh) return;
+    c.bh = 0;
+    if (++c.bd < a.nbd) return;
+    c.bd = 0;
+    ++c.n;
+  };
+  // Loads of one box into the staging registers.  A box whose tile lies
+  // inside the volume (the common case) takes the precomputed validity; one
+  // on an edge checks every item's position (branch-free).
+  auto issue = [&](const BoxCur& cur) __attribute__((always_inline)) {
+    const int r0d = cur.bd * Geo::TD, r0h = cur.bh * TH, r0w = cur.bw * 16;
     int s0d, s0h, s0w;
     if (MODE == MODE_T2DW) {
       s0d = 2 * r0d;
@@ -193,42 +250,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       s0h = r0h - a.ph;
       s0w = r0w - a.pw;
     }
-    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (int64_t)n * a.fs[0], a.f_bytes);
-    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (int64_t)n * a.gs[0], a.g_bytes);
+    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (int64_t)cur.n * a.fs[0], a.f_bytes);
+    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (int64_t)cur.n * a.gs[0], a.g_bytes);
+    const int fbase = 2 * (r0d * fs2 + r0h * fs3 + r0w * fs4);
+    const int gbase = 2 * (s0d * gs2 + s0h * gs3 + s0w * gs4);
+    const bool f_in = r0d + Geo::TD <= a.Rd && r0h + TH <= a.Rh && r0w + 16 <= a.Rw;
+    const bool g_in = s0d >= 0 && s0d + Geo::HD <= a.Gd && s0h >= 0 && s0h + HH <= a.Gh && s0w >= 0 &&
+                      s0w + (FL == 2 ? 16 : HW) <= a.Gw;
 #pragma unroll
     for (int k = 0; k < NFI; ++k) {
       const int c = fcode[k];
-      const int td = c & 255, th = (c >> 8) & 255, tw = (c >> 16) & 255, cg = c >> 24;
-      const int gd = r0d + td, gh = r0h + th, gw = r0w + tw;
-      if (FL >= 1) {  // 8 positions gw .. gw+7 of channel fc0 + cg (the planner keeps Rw % 8 == 0)
-        const int ch = fc0 + cg;
-        const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && ch < a.Fc;
-        const int off = 2 * (gd * fs2 + gh * fs3 + gw + ch * fs1);
-        pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, ok ? off : kOob, 0, 0));
-      } else {
-        const int c0 = fc0 + cg * 8;
-        const bool ok = c >= 0 && gd < a.Rd && gh < a.Rh && gw < a.Rw && c0 < a.Fc;
-        const int off = 2 * (gd * fs2 + gh * fs3 + gw * fs4 + c0 * fs1);
-        pf[k] = load8(fsrc, ok, off, a.Fc - c0, fs1);
+      bool ok = fval[k];
+      if (!f_in) {
+        const int gd = r0d + (c & 255), gh = r0h + ((c >> 8) & 255), gw = r0w + ((c >> 16) & 255);
+        ok = ok & (gd < a.Rd) & (gh < a.Rh) & (gw < a.Rw);
       }
+      const int off = fbase + frel[k];
+      if (FL >= 1) pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, ok ? off : kOob, 0, 0));
+      else pf[k] = load8(fsrc, ok, off, fcv[k], fs1);
     }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
       const int c = gcode[k];
-      if (FL == 2) {  // 8 positions of channel gc0 + ch (k=1 without padding: G sits on the F grid)
+      bool ok = gval[k];
+      if (!g_in) {
         const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = s0w + ((c >> 16) & 255);
-        const int ch = gc0 + (c >> 24);
-        const bool ok = c >= 0 && gd < a.Gd && gh < a.Gh && gw < a.Gw && ch < a.Gc;
-        const int off = 2 * (gd * gs2 + gh * gs3 + gw + ch * gs1);
-        pg[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, ok ? off : kOob, 0, 0));
-        continue;
+        ok = ok & ((unsigned)gd < (unsigned)a.Gd) & ((unsigned)gh < (unsigned)a.Gh) & ((unsigned)gw < (unsigned)a.Gw);
       }
-      const int hd = c & 255, hh = (c >> 8) & 255, hw = (c >> 16) & 255, cg = c >> 24;
-      const int gd = s0d + hd, gh = s0h + hh, gw = s0w + hw, c0 = gc0 + cg * 8;
-      const bool ok = c >= 0 && (unsigned)gd < (unsigned)a.Gd && (unsigned)gh < (unsigned)a.Gh &&
-                      (unsigned)gw < (unsigned)a.Gw && c0 < a.Gc;
-      const int off = 2 * (gd * gs2 + gh * gs3 + gw * gs4 + c0 * gs1);
-      pg[k] = load8(gsrc, ok, off, a.Gc - c0, gs1);
+      const int off = gbase + grel[k];
+      if (FL == 2) pg[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, ok ? off : kOob, 0, 0));
+      else pg[k] = load8(gsrc, ok, off, gcv[k], gs1);
     }
   };
   auto commit = [&](int buf) {
@@ -262,24 +313,76 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   int go[CBW];
 #pragma unroll
   for (int q = 0; q < CBW; ++q) go[q] = WS * tw0 * 32 + goff[q];
-
-  if (box_begin < box_end) {
-    issue(box_begin);
-    commit(0);
-    if (box_begin + 1 < box_end) issue(box_begin + 1);
-  }
-  for (int box = box_begin; box < box_end; ++box) {
-    const int buf = (box - box_begin) & 1;
-    __syncthreads();  // buffer buf is complete; buffer buf^1 is no longer read
-    if (box + 1 < box_end) {
-      commit(buf ^ 1);
-      if (box + 2 < box_end) issue(box + 2);  // in flight during the K loop
-    }
-    const uint16_t* ftile = tiles + buf * TILE;
-    const uint16_t* gtile = ftile + FT;
-
+  // Column blocks of this wave (blocks wv, wv + 8, ...): a prefix of q.
+  int nv = 0;
 #pragma unroll
-    for (int st = 0; st < Geo::LINES; ++st) {
+  for (int q = 0; q < CBW; ++q) nv += cbok[q] ? 1 : 0;
+
+  // Pipeline: box i computes from buffer i % 2.  After the barrier and the
+  // first step, box i+1's registers go to the other buffer and box i+2's loads
+  // are issued into them, inside the MFMA stream.  The barrier waits for LDS
+  // traffic only, so those loads stay in flight across it.
+  const int nbx = box_end - box_begin;
+  BoxCur ca = box_at(box_begin < box_end ? box_begin : 0);
+  if (nbx > 0) {
+    issue(ca);
+    box_advance(ca);
+    commit(0);
+    if (nbx > 1) {
+      issue(ca);
+      box_advance(ca);
+    }
+  }
+  constexpr int HOOK = 1;
+  // K loop of one box with NV column blocks and, with DBF, the bias MFMA.
+  auto run_box = [&](int i, auto buf_c, auto nv_c, auto dbf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
+    constexpr int NV = decltype(nv_c)::value;
+    constexpr bool DBF = decltype(dbf_c)::value;
+    const uint16_t* ftile = tiles + BUF * TILE;
+    const uint16_t* gtile = ftile + FT;
+    uint4 ffr[2], gfr[2][NV > 0 ? NV : 1];
+    auto read_step = [&](auto st_c, int slot) __attribute__((always_inline)) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int TD_ = ST / TH, TH_ = ST % TH;
+      constexpr int FROW = ST * 16 * 32;
+      constexpr int GROW = ((WS * TD_) * HH + WS * TH_) * HW * 32;
+      ffr[slot] = FL >= 1 ? *reinterpret_cast<const uint4*>(ftile + li * FP + ST * 16 + 8 * g)
+                          : lds_tr_pair(ftile, fo + FROW, fo + FROW + 4 * 32);
+#pragma unroll
+      for (int q = 0; q < NV; ++q)
+        gfr[slot][q] = FL == 2 ? *reinterpret_cast<const uint4*>(gtile + ((q * 8 + wv) * 32 + li) * FP + ST * 16 + 8 * g)
+                               : lds_tr_pair(gtile, go[q] + GROW, go[q] + GROW + WS * 4 * 32);
+    };
+    auto step = [&](auto st_c) __attribute__((always_inline)) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int CUR = ST & 1;
+      if constexpr (ST + 1 < LINES) read_step(std::integral_constant<int, ST + 1>{}, CUR ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (DBF) accf = mfma32<T>(ffr[CUR], ones, accf);
+#pragma unroll
+      for (int q = 0; q < NV; ++q) acc[q] = mfma32<T>(ffr[CUR], gfr[CUR][q], acc[q]);
+      if constexpr (ST == HOOK) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < nbx) commit(BUF ^ 1);
+        if (i + 2 < nbx) {
+          issue(ca);
+          box_advance(ca);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    read_step(std::integral_constant<int, 0>{}, 0);
+    static_for(std::make_integer_sequence<int, LINES>{}, step);
+  };
+  // The generic box (ConvTranspose, or an uncommon block split) tests each
+  // block per step.
+  auto run_box_generic = [&](int i, auto buf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
+    const uint16_t* ftile = tiles + BUF * TILE;
+    const uint16_t* gtile = ftile + FT;
+#pragma unroll
+    for (int st = 0; st < LINES; ++st) {
       const int td = st / TH, th = st % TH;
       const int frow = st * 16 * 32;
       const int grow = ((WS * td) * HH + WS * th) * HW * 32;
@@ -296,7 +399,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
           if (do_dbg) accg[q < NDBG ? q : 0] = mfma32<T>(ones, gfr, accg[q < NDBG ? q : 0]);
         }
       }
+      if (st == HOOK) {
+        if (i + 1 < nbx) commit(BUF ^ 1);
+        if (i + 2 < nbx) {
+          issue(ca);
+          box_advance(ca);
+        }
+      }
     }
+  };
+  // 0: full blocks, 1: one block fewer, 2: full + bias, 3: one fewer + bias, 4: generic.
+  const int kind = (MODE == MODE_T2DW || CBW < 2) ? 4
+                   : nv == CBW                  ? (do_dbf ? 2 : 0)
+                   : nv == CBW - 1              ? (do_dbf ? 3 : 1)
+                                                : 4;
+  auto run = [&](int i, auto buf_c) __attribute__((always_inline)) {
+    lds_barrier();  // buffer i%2 complete; buffer (i+1)%2 no longer read
+    using NF = std::integral_constant<int, (CBW >= 2 ? CBW : 1)>;
+    using NL = std::integral_constant<int, (CBW >= 2 ? CBW - 1 : 1)>;
+    if (MODE != MODE_T2DW && CBW >= 2 && kind == 0) run_box(i, buf_c, NF{}, std::false_type{});
+    else if (MODE != MODE_T2DW && CBW >= 2 && kind == 1) run_box(i, buf_c, NL{}, std::false_type{});
+    else if (MODE != MODE_T2DW && CBW >= 2 && kind == 2) run_box(i, buf_c, NF{}, std::true_type{});
+    else if (MODE != MODE_T2DW && CBW >= 2 && kind == 3) run_box(i, buf_c, NL{}, std::true_type{});
+    else run_box_generic(i, buf_c);
+  };
+  for (int i = 0; i < nbx; i += 2) {
+    run(i, std::integral_constant<int, 0>{});
+    if (i + 1 < nbx) run(i + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- partial store: acc[q][4qq + r] = C[f = 8qq + 4g + r][column li of block]
