@@ -13,8 +13,12 @@ Also reported on the same JSON line:
   roofline      the dominant kernel (largest share of the step): algorithmic FLOPs
                 per launch / its average launch duration, measured live with HIP
                 events on its launch stream (the library's timing hook) during the
-                timed steps, against the 2.5 PFLOP/s dense bf16 MFMA peak.
-  passes        per-pass kernel time and fraction of peak.
+                timed steps, against the 2.5 PFLOP/s dense bf16 MFMA peak.  Only
+                that kernel's launches carry events in the timed steps, so the
+                hook does not slow the step it measures.
+  passes        per-pass kernel time and fraction of peak, from a few untimed
+                steps before the timed region in which every launch carries events
+                (these also pick the dominant kernel).
   hbm_passes    BASELINE configs 3 and 4 (k=1 fp16, ConvTranspose3d k2s2 bf16):
                 per-pass time (all kernels of the pass, median of 20, MALL
                 flushed before each) and compulsory HBM bytes / time vs 8 TB/s.
@@ -296,6 +300,45 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     }
 
 
+def traffic_probe(name: str, layout: str) -> int:
+    """Kernels for an HBM-traffic measurement (run under rocprofv3 --pmc): a
+    256 MiB device copy three times (FETCH_SIZE / WRITE_SIZE calibration), then
+    the trunk pass `name` (k3_<ci>to<co>_<fwd|dx|dw>) three times."""
+    import torch
+    from rdna4_conv3d import _native as nat
+    dev = torch.device("cuda", 0)
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    stem, p = name.rsplit("_", 1)
+    for (n, ci, co, d, h, w) in TRUNK:
+        if stem == f"k3_{ci}to{co}":
+            break
+    else:
+        print(f"bench.py: unknown probe pass {name}", file=sys.stderr)
+        return 2
+
+    def L(t):
+        return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
+    x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
+    go = L(_gen((n, co, d, h, w), 2, torch.bfloat16).to(dev))
+    wt = _kaiming((co, ci, 3, 3, 3), ci * 27, 1, torch.bfloat16).to(dev)
+    bias = _kaiming((co,), ci * 27, 3, torch.bfloat16).to(dev)
+    for _ in range(3):
+        if p == "fwd":
+            nat.conv3d_fwd(x, wt, bias, (1, 1, 1))
+        elif p == "dx":
+            nat.conv3d_dx(go, wt, x.shape, (1, 1, 1), like=x)
+        else:
+            nat.conv3d_dw(x, go, wt.shape, (1, 1, 1), torch.float32, want_db=True, db_dtype=torch.float32)
+    torch.cuda.synchronize()
+    print(f"probe {name} {layout} done", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -306,6 +349,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--unet-steps", type=int, default=40, help="UNet3D config-5 timed steps (0 skips it)")
     ap.add_argument("--no-hbm-passes", action="store_true", help="skip the k=1 / ConvTranspose3d passes")
+    ap.add_argument("--probe", default=None, metavar="PASS",
+                    help="traffic probe for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB Tensor.copy_ (the "
+                         "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd; exits")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="diagnostic: time the step without the per-launch event hook (no roofline/passes)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -332,6 +380,9 @@ def main() -> int:
     def L(t):
         return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
 
+    if args.probe:
+        return traffic_probe(args.probe, layout)
+
     layers = []
     for li, (n, ci, co, d, h, w) in enumerate(TRUNK):
         x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
@@ -354,8 +405,51 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
-    nat.timing_enable(True)
-    nat.timing_collect()
+    step_flops = 3 * sum(l[4] for l in layers)
+
+    # Kernel profile: every launch of a few untimed steps is bracketed by HIP
+    # events on its launch stream -> per-pass kernel times and the dominant
+    # kernel (largest share of the step).
+    passes = {}
+    dominant = None
+    if not args.no_kernel_timing:
+        nat.timing_filter(-1, None)
+        nat.timing_enable(True)
+        nat.timing_collect()
+        for _ in range(max(3, min(args.steps, 10))):
+            step()
+        torch.cuda.synchronize()
+        recs = nat.timing_collect()
+        nat.timing_enable(False)
+        per = {}
+        for tag, kind, ms in recs:
+            per.setdefault((tag, kind), []).append(ms)
+        for li, (n, ci, co, d, h, w) in enumerate(TRUNK):
+            for pi, p in enumerate(PASSES):
+                tag = li * 3 + pi
+                main_kind = "wgrad" if p == "dw" else "row"
+                main = per.get((tag, main_kind), [])
+                aux = sum(sum(v) for (t, k), v in per.items() if t == tag and k != main_kind) / max(1, len(main))
+                if not main:
+                    continue
+                avg = sum(main) / len(main)
+                fl = layers[li][4]
+                name = f"k3_{ci}to{co}_{d}x{h}x{w}_{p}"
+                passes[name] = {
+                    "kernel_us": round(avg * 1e3, 2),
+                    "aux_us": round(aux * 1e3, 2),
+                    "tflops": round(fl / (avg * 1e-3) / 1e12, 1),
+                    "frac_mfma": round(fl / (avg * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                }
+                share = avg * len(main)
+                if dominant is None or share > dominant[0]:
+                    dominant = (share, name, tag, main_kind, fl)
+        # Timed region: only the dominant kernel's launches carry events, so
+        # the hook does not slow the step it measures.
+        nat.timing_filter(dominant[2], dominant[3])
+        nat.timing_enable(True)
+        nat.timing_collect()
+
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -366,40 +460,19 @@ def main() -> int:
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    drecs = nat.timing_collect() if not args.no_kernel_timing else []
     nat.timing_enable(False)
-    recs = nat.timing_collect()
+    nat.timing_filter(-1, None)
     ms_step = e0.elapsed_time(e1) / args.steps
-    step_flops = 3 * sum(l[4] for l in layers)
     value = step_flops / (ms_step * 1e-3) / 1e12
 
-    # Per-pass kernel times from the live event records.
-    per = {}
-    for tag, kind, ms in recs:
-        key = (tag, kind)
-        per.setdefault(key, []).append(ms)
-    passes = {}
-    dominant = None
-    for li, (n, ci, co, d, h, w) in enumerate(TRUNK):
-        for pi, p in enumerate(PASSES):
-            tag = li * 3 + pi
-            main_kind = "wgrad" if p == "dw" else "row"
-            main = per.get((tag, main_kind), [])
-            aux = sum(sum(v) for (t, k), v in per.items() if t == tag and k != main_kind) / max(1, len(main))
-            if not main:
-                continue
-            avg = sum(main) / len(main)
-            fl = layers[li][4]
-            name = f"k3_{ci}to{co}_{d}x{h}x{w}_{p}"
-            passes[name] = {
-                "kernel_us": round(avg * 1e3, 2),
-                "aux_us": round(aux * 1e3, 2),
-                "tflops": round(fl / (avg * 1e-3) / 1e12, 1),
-                "frac_mfma": round(fl / (avg * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-            }
-            share = avg * len(main)
-            if dominant is None or share > dominant[0]:
-                dominant = (share, name, avg, fl)
-    _, dname, davg, dfl = dominant
+    if dominant is None:  # --no-kernel-timing
+        print(json.dumps({"metric": "step time without the kernel timing hook (diagnostic)",
+                          "ms_per_step": round(ms_step, 4), "value": round(value, 2), "unit": "TFLOP/s"}), flush=True)
+        return 0
+    _, dname, _, _, dfl = dominant
+    dms = [ms for _, _, ms in drecs if ms > 0]
+    davg = sum(dms) / len(dms)
     achieved = dfl / (davg * 1e-3) / 1e12
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
@@ -417,6 +490,7 @@ def main() -> int:
         "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
         "traffic": traffic,
         "avg_launch_us": round(davg * 1e3, 2),
+        "launches_timed": len(dms),
         "flops_per_launch": dfl,
     }
 

@@ -141,9 +141,12 @@ int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* desc, const void* x,
  * 4 NCDHW-to-NDHWC copy, 5 row-kernel split-K epilogue pass).
  * r3c_timing_collect waits for the recorded events, writes up to max_records
  * (tag, kind, milliseconds) triples, clears the records and returns how many
- * launches were recorded. */
+ * launches were recorded.  r3c_timing_filter limits recording to launches
+ * with the given tag and kind (-1 = any; the default), so one kernel can be
+ * timed inside a run without bracketing every other launch. */
 int32_t r3c_timing_enable(int32_t on);
 void r3c_timing_set_tag(int32_t tag);
+void r3c_timing_filter(int32_t tag, int32_t kind);
 int32_t r3c_timing_collect(int32_t max_records, int32_t* tags, int32_t* kinds, float* ms);
 
 #ifdef __cplusplus

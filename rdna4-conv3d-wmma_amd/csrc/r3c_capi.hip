@@ -127,6 +127,7 @@ struct TimingRec {
 struct TimingState {
   std::mutex mu;
   bool on = false;
+  int filter_tag = -1, filter_kind = -1;  // record only matching launches (-1 = any)
   std::vector<TimingRec> recs;
   std::vector<hipEvent_t> pool;
 };
@@ -158,6 +159,7 @@ struct TimedLaunch {
   TimedLaunch(int k, hipStream_t stream) : st(timing()), s(stream), kind(k) {
     std::lock_guard<std::mutex> lk(st.mu);
     if (!st.on) return;
+    if ((st.filter_tag >= 0 && st.filter_tag != g_tag) || (st.filter_kind >= 0 && st.filter_kind != k)) return;
     e0 = pool_event(st);
     if (e0 && hipEventRecord(e0, s) == hipSuccess) active = true;
   }
@@ -965,6 +967,13 @@ int32_t r3c_timing_enable(int32_t on) {
 }
 
 void r3c_timing_set_tag(int32_t tag) { g_tag = tag; }
+
+void r3c_timing_filter(int32_t tag, int32_t kind) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  st.filter_tag = tag;
+  st.filter_kind = kind;
+}
 
 int32_t r3c_timing_collect(int32_t max_records, int32_t* tags, int32_t* kinds, float* ms) {
   TimingState& st = timing();

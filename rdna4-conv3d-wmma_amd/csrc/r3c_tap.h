@@ -80,10 +80,12 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, S...>, F&&
 
 struct TapCursor {
   int chunk, split, ct, bw, bh, bd, n;
+  int job;  // job index (the workgroup takes jobs job, job + stride, ...)
 };
 
 __device__ __forceinline__ TapCursor tap_cursor_at(const RowArgs& a, int job) {
   TapCursor c;
+  c.job = job;
   c.split = job % a.nsplit;
   c.chunk = c.split * a.cps;
   const int tile = job / a.nsplit;
@@ -98,20 +100,10 @@ __device__ __forceinline__ TapCursor tap_cursor_at(const RowArgs& a, int job) {
   return c;
 }
 
-__device__ __forceinline__ void tap_advance(const RowArgs& a, TapCursor& c) {
+// Next stage: the next chunk of the job, else the first chunk of job + stride.
+__device__ __forceinline__ void tap_advance(const RowArgs& a, TapCursor& c, int stride) {
   if (++c.chunk < (c.split + 1) * a.cps) return;
-  if (++c.split < a.nsplit) return;  // chunk is already split * cps
-  c.split = 0;
-  c.chunk = 0;
-  if (++c.ct < a.n_ctiles) return;
-  c.ct = 0;
-  if (++c.bw < a.nbw) return;
-  c.bw = 0;
-  if (++c.bh < a.nbh) return;
-  c.bh = 0;
-  if (++c.bd < a.nbd) return;
-  c.bd = 0;
-  ++c.n;
+  c = tap_cursor_at(a, c.job + stride);
 }
 
 // Output tile (box, column tile) of a cursor.
@@ -260,13 +252,21 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   float* btab = reinterpret_cast<float*>(reinterpret_cast<char*>(wts + wslots) + G::SCR_BYTES);
   const int nbcol = a.nbt_pad * 32;
 
-  // Contiguous job range; XCD-aware numbering (workgroups are dealt to the 8
-  // XCDs round-robin, so renumber to give each XCD a contiguous eighth).
+  // Job assignment.  Workgroups are dealt to the 8 XCDs round-robin; each XCD
+  // owns a contiguous eighth of the jobs, and inside it its workgroups take
+  // jobs round-robin (job = first + i + k * nx).  The workgroups running at
+  // the same time then work on neighbouring boxes, whose shared halo rows meet
+  // in the XCD's L2 instead of being fetched once per box.
   const int nwg = gridDim.x;
-  const int wg = (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
-  const int j0 = (int)(((int64_t)wg * a.njobs) / nwg);
-  const int j1 = (int)(((int64_t)(wg + 1) * a.njobs) / nwg);
-  if (j0 >= j1) return;
+  const bool byxcd = (nwg & 7) == 0;
+  const int xcd = byxcd ? (int)(blockIdx.x & 7) : 0;
+  const int nx = byxcd ? nwg >> 3 : nwg;
+  const int wi = byxcd ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int jx0 = (int)(((int64_t)xcd * a.njobs) / (byxcd ? 8 : 1));
+  const int jx1 = (int)(((int64_t)(xcd + 1) * a.njobs) / (byxcd ? 8 : 1));
+  const int j0 = jx0 + wi;
+  if (j0 >= jx1) return;
+  const int myjobs = (jx1 - j0 + nx - 1) / nx;
 
   for (int c = tid; c < nbcol; c += 512) btab[c] = (a.bias && c < a.ncols) ? to_f32<T>(a.bias[c]) : 0.f;
 
@@ -443,29 +443,29 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   // Prologue: stages 0 .. DIST-1 into register sets 0 .. DIST-1, stage 0
   // into buffer 0, stage DIST into set 0; weights of stage 0 into buffer 0,
   // stage 1 in flight.
-  const int nstage = (j1 - j0) * a.cps;
+  const int nstage = myjobs * a.cps;
   TapCursor cc = tap_cursor_at(a, j0);
   TapCursor ca = cc, cw = cc;
   issue_act(ca, 0);
-  tap_advance(a, ca);
+  tap_advance(a, ca, nx);
   if (DIST == 2 && nstage > 1) {
     issue_act(ca, DIST - 1);
-    tap_advance(a, ca);
+    tap_advance(a, ca, nx);
   }
   if (!WF) {
     issue_w(cw);
-    tap_advance(a, cw);
+    tap_advance(a, cw, nx);
   }
   commit_act(0, 0);
   if (nstage > DIST) {
     issue_act(ca, 0);
-    tap_advance(a, ca);
+    tap_advance(a, ca, nx);
   }
   if (!WF) {
     commit_w(0);
     if (nstage > 1) {
       issue_w(cw);
-      tap_advance(a, cw);
+      tap_advance(a, cw, nx);
     }
   }
 
@@ -501,13 +501,13 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
         if (t + 1 < nstage) commit_act(SN, 1 - BUF);
         if (t + 1 + DIST < nstage) {
           issue_act(ca, SN);
-          tap_advance(a, ca);
+          tap_advance(a, ca, nx);
         }
         if (!WF) {
           if (t + 1 < nstage) commit_w(1 - BUF);
           if (t + 2 < nstage) {
             issue_w(cw);
-            tap_advance(a, cw);
+            tap_advance(a, cw, nx);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -526,7 +526,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
     }
-    tap_advance(a, cc);
+    tap_advance(a, cc, nx);
   };
   for (int t = 0; t < nstage; t += 2) {
     run_stage(t, std::integral_constant<int, 0>{});

@@ -83,8 +83,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   bid /= a.n_ftiles;
   const int gt = bid % a.n_gtiles;
   const int split = bid / a.n_gtiles;
-  const int box_begin = (int)(((int64_t)split * a.nbox) / a.nsplit);
-  const int box_end = (int)(((int64_t)(split + 1) * a.nbox) / a.nsplit);
+  // Boxes of this split.  With a multiple of 8 splits, the splits of one XCD
+  // (consecutive split indices) share a contiguous eighth of the boxes and take
+  // them round-robin (box = first + si + k * s8): the workgroups running at the
+  // same time then work on neighbouring boxes, whose halos meet in the XCD's
+  // L2.  The assignment is fixed, so the sums stay deterministic.
+  const bool sg8 = (a.nsplit & 7) == 0;
+  const int s8 = sg8 ? a.nsplit >> 3 : 1;
+  const int sgrp = sg8 ? split / s8 : split, si = sg8 ? split % s8 : 0;
+  const int ngrp = sg8 ? 8 : a.nsplit;
+  const int gb0 = (int)(((int64_t)sgrp * a.nbox) / ngrp);
+  const int gb1 = (int)(((int64_t)(sgrp + 1) * a.nbox) / ngrp);
+  const int box_begin = gb0 + si;
 
   uint16_t* const tiles = reinterpret_cast<uint16_t*>(smem4);  // [2][F tile, G tile]
 
@@ -214,10 +224,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 
   // Box cursor (w fastest), advanced by carries: the divisions happen once.
   struct BoxCur {
-    int bw, bh, bd, n;
+    int bw, bh, bd, n, box;
   };
   auto box_at = [&](int box) {
     BoxCur c;
+    c.box = box;
     c.bw = box % a.nbw;
     box /= a.nbw;
     c.bh = box % a.nbh;
@@ -227,6 +238,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     return c;
   };
   auto box_advance = [&](BoxCur& c) {
+    if (s8 != 1) {
+      c = box_at(c.box + s8);
+      return;
+    }
+    ++c.box;
     if (++c.bw < a.nbw) return;
     c.bw = 0;
     if (++c.bh < a.nbh) return;
@@ -322,8 +338,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   // first step, box i+1's registers go to the other buffer and box i+2's loads
   // are issued into them, inside the MFMA stream.  The barrier waits for LDS
   // traffic only, so those loads stay in flight across it.
-  const int nbx = box_end - box_begin;
-  BoxCur ca = box_at(box_begin < box_end ? box_begin : 0);
+  const int nbx = box_begin < gb1 ? (gb1 - box_begin + s8 - 1) / s8 : 0;
+  BoxCur ca = box_at(box_begin < gb1 ? box_begin : 0);
   if (nbx > 0) {
     issue(ca);
     box_advance(ca);

@@ -91,6 +91,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_timing_enable.argtypes = [I32]
     lib.r3c_timing_set_tag.restype = None
     lib.r3c_timing_set_tag.argtypes = [I32]
+    lib.r3c_timing_filter.restype = None
+    lib.r3c_timing_filter.argtypes = [I32, I32]
     lib.r3c_timing_collect.restype = I32
     lib.r3c_timing_collect.argtypes = [I32, ctypes.POINTER(I32), ctypes.POINTER(I32), ctypes.POINTER(ctypes.c_float)]
 
@@ -143,6 +145,11 @@ def timing_enable(on: bool) -> None:
 def timing_tag(tag: int) -> None:
     """Tag attached to the kernels this thread launches next."""
     load().r3c_timing_set_tag(int(tag))
+
+
+def timing_filter(tag: int = -1, kind: Optional[str] = None) -> None:
+    """Record only launches with this tag and kernel kind name (-1 / None = any)."""
+    load().r3c_timing_filter(int(tag), -1 if kind is None else KERNEL_KINDS.index(kind))
 
 
 def timing_collect(max_records: int = 1 << 16):
