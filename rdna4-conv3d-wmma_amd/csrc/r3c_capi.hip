@@ -382,7 +382,7 @@ TapBox tap_box(int mb, int lw) {
   b.HPAD = (b.HPOS + 15) / 16 * 16;
   return b;
 }
-constexpr int64_t kTapScratch = 8 * 32 * 40 * 2;  // epilogue scratch of the 8 waves
+constexpr int64_t kTapScratch = 0;               // the epilogue stores from registers
 constexpr int kTapStep = 14;                      // MFMA steps per 8-channel chunk (27 taps)
 
 // Conv3d k=3 plan on the tap kernel; `a` already holds the source/destination
@@ -517,6 +517,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
     channels_last_strides(a.ss, cs, sdd, sh, sw);
   }
   a.src_bytes = sample_bytes(a.ss, cs, sdd, sh, sw);
+  a.dst_bytes = sample_bytes(a.sd, a.ncols, a.Rd, a.Rh, a.Rw);
   // Channel-contiguous sources are staged by direct-to-LDS 16-byte loads;
   // others by 8 scalar loads per slot through registers.
   p.cl = (a.ss[1] == 1 && cs % 8 == 0 && a.ss[0] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 &&
@@ -617,6 +618,8 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   plan_row(d, op, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
   if (p.a.src_bytes == 0) return fail(R3C_UNSUPPORTED, "one input sample exceeds 1 GiB (32-bit buffer offsets)");
+  if (p.tap && p.a.dst_bytes == 0)
+    return fail(R3C_UNSUPPORTED, "one output sample exceeds 1 GiB (32-bit buffer offsets)");
   const int64_t need = align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);

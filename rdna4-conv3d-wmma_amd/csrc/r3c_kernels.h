@@ -31,6 +31,7 @@ struct RowArgs {
   int64_t ss[5];         // source strides (n, c, d, h, w)
   int64_t sd[5];         // destination strides (n, c, d, h, w)
   uint32_t src_bytes;    // bytes of one source sample reachable from its base (buffer range)
+  uint32_t dst_bytes;    // the same for one destination sample (k=3 tap kernel stores)
   int32_t Cs, Sd, Sh, Sw;  // source channels and spatial dims
   int32_t Rd, Rh, Rw;      // row grid (destination grid; source grid for T2FWD)
   int32_t pd, ph, pw;      // Conv3d padding (K1/K3)

@@ -58,8 +58,6 @@ struct TapGeom {
   static constexpr int HPOS = HD * HH * HW;
   static constexpr int HPAD = (HPOS + 15) / 16 * 16;  // slots per activation buffer
   static constexpr int MAXK = (HPOS + NT - 1) / NT;   // staging slots per thread
-  static constexpr int SP = 40;                       // epilogue scratch pitch (halves): 2-way banks at most
-  static constexpr int SCR_BYTES = NW * 32 * SP * 2;
   // Slot offset of tap t in the tile.
   static constexpr int tap_off(int t) { return ((t / 9) * HH + (t / 3) % 3) * HW + t % 3; }
   // Step s pairs taps 2s (g = 0) and 2s + 1 (g = 1; the 28th is K padding with
@@ -111,97 +109,70 @@ __device__ __forceinline__ int tap_tile(const RowArgs& a, const TapCursor& c) {
   return (((c.n * a.nbd + c.bd) * a.nbh + c.bh) * a.nbw + c.bw) * a.n_ctiles + c.ct;
 }
 
-// Epilogue of one wave: its MB x NB C tiles (+ bias) -> 16-bit -> scratch
-// [column][position] (pitch SP) -> 16-byte global stores in the destination's
-// layout: 8 consecutive positions of a channel per lane when positions are
-// contiguous (NCDHW), or, through ds_read_tr16_b64, 8 consecutive channels of
-// a position when channels are (NDHWC).  Lane (g, i) of a C tile holds rows
-// 8q + 4g + r (positions of the line) of column i.  btab[c - bcol0] is the
-// bias of column c.
+// Epilogue of one wave, straight from registers.  The MFMAs compute C^T (A =
+// weights, B = activations), so lane (g, i) of a tile holds columns
+// (output channels) 8q + 4g + r, q, r in 0..3, of row (position) i of its
+// line: acc[4q + r].  With positions contiguous in memory (NCDHW) a 2-byte
+// store per (q, r) writes 32 consecutive positions of a channel per half-wave;
+// with channels contiguous (NDHWC) an 8-byte store per q writes 4 channels of
+// a position.  Stores go through a buffer resource over the output sample;
+// lanes outside the volume or past the last column get an offset with bit 31
+// set (past num_records: dropped).  btab[c - bcol0] is the bias of column c.
 template <typename T, int NB, int MB, int LW>
 __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[MB][NB], int wv, int lane,
-                                             const TapCursor& ec, uint16_t* scr, const float* btab, int bcol0) {
+                                             const TapCursor& ec, const float* btab, int bcol0) {
   constexpr int HR = TapGeom<MB, LW>::HR;
-  constexpr int SP = TapGeom<MB, LW>::SP;
-  const int g = lane >> 5, li = lane & 31;
   constexpr int TD = TapGeom<MB, LW>::TD, TH = TapGeom<MB, LW>::TH;
+  const int g = lane >> 5, li = lane & 31;
   const int r0d = ec.bd * TD, r0h = ec.bh * TH * HR, r0w = ec.bw * LW;
   const int64_t* sd = a.sd;
-  uint16_t* dstn = a.dst + (int64_t)ec.n * sd[0];
+  const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.dst + (int64_t)ec.n * sd[0], a.dst_bytes);
   const bool pos_contig = sd[4] == 1;
   const bool ch_contig = !pos_contig && sd[1] == 1;
+  const int sd1 = (int)sd[1], sd2 = (int)sd[2], sd3 = (int)sd[3], sd4 = (int)sd[4];
+  auto gate = [](uint32_t off, bool on) { return (int)(off | ((uint32_t)!on << 31)); };
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int r = wv * MB + mb;
     const int td = r / TH, th = r % TH;
-    const int rd = r0d + td, rh = r0h + th * HR;
-    if (rd >= a.Rd || rh >= a.Rh) continue;
-    uint16_t* plane = dstn + (int64_t)rd * sd[2];
+    const int rd = r0d + td;
+    const int h = r0h + th * HR + li / LW, w = r0w + li % LW;  // this lane's position
+    const bool pos_ok = rd < a.Rd && h < a.Rh && w < a.Rw;
+    const uint32_t poff = 2u * (uint32_t)(rd * sd2 + h * sd3 + w * sd4);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int colbase = (ec.ct * NB + nb) * 32;
       if (colbase >= a.ncols) continue;
-      {
-        const float bv = btab[colbase - bcol0 + li];
+      const float4* bt = reinterpret_cast<const float4*>(btab + (colbase - bcol0)) + g;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint2 v;
-          v.x = pack2(from_f32<T>(acc[mb][nb][4 * q + 0] + bv), from_f32<T>(acc[mb][nb][4 * q + 1] + bv));
-          v.y = pack2(from_f32<T>(acc[mb][nb][4 * q + 2] + bv), from_f32<T>(acc[mb][nb][4 * q + 3] + bv));
-          *reinterpret_cast<uint2*>(scr + li * SP + 8 * q + 4 * g) = v;
-        }
-      }
-      // A wave's LDS operations execute in order; only the compiler must be
-      // kept from moving the reads above the writes.
-      __builtin_amdgcn_wave_barrier();
-      if (pos_contig) {
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = colbase + 8 * q + 4 * g;  // channels c0 .. c0+3 of this lane
+        if (colbase + 8 * q >= a.ncols) break;   // uniform: the rest of the block is padding
+        const float4 bv = bt[2 * q];
+        const float v0 = acc[mb][nb][4 * q + 0] + bv.x, v1 = acc[mb][nb][4 * q + 1] + bv.y;
+        const float v2 = acc[mb][nb][4 * q + 2] + bv.z, v3 = acc[mb][nb][4 * q + 3] + bv.w;
+        if (pos_contig || !ch_contig) {
+          const float vv[4] = {v0, v1, v2, v3};
 #pragma unroll
-        for (int rd2 = 0; rd2 < 2; ++rd2) {
-          const int id = rd2 * 64 + lane;
-          const int c = id >> 2, p0 = (id & 3) * 8;
-          const int col = colbase + c;
-          const int h = rh + p0 / LW, w = r0w + p0 % LW;
-          const uint4 v = *reinterpret_cast<const uint4*>(scr + c * SP + p0);
-          if (col < a.ncols && h < a.Rh && w < a.Rw) {
-            uint16_t* p = plane + (int64_t)col * sd[1] + (int64_t)h * sd[3] + w;
-            if (w + 8 <= a.Rw && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
-              *reinterpret_cast<uint4*>(p) = v;
-            } else {
-              for (int k = 0; k < 8 && w + k < a.Rw; ++k) p[k] = u4_elem(v, k);
-            }
+          for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t off = poff + 2u * (uint32_t)((c0 + rr) * sd1);
+            __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off, pos_ok && c0 + rr < a.ncols), 0, 0);
+          }
+        } else {
+          typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+          const uint32_t off = poff + 2u * (uint32_t)c0;
+          if (c0 + 4 <= a.ncols) {
+            const u32x2_t v = {pack2(from_f32<T>(v0), from_f32<T>(v1)), pack2(from_f32<T>(v2), from_f32<T>(v3))};
+            __builtin_amdgcn_raw_buffer_store_b64(v, dst, gate(off, pos_ok), 0, 0);
+          } else {
+            const float vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off + 2u * rr, pos_ok && c0 + rr < a.ncols),
+                                                    0, 0);
           }
         }
-      } else if (ch_contig) {
-        const int sl = lane & 15;
-#pragma unroll
-        for (int rd2 = 0; rd2 < 2; ++rd2) {
-          const int task = rd2 * 4 + (lane >> 4);
-          const int p0 = 16 * (task & 1), c0 = 8 * (task >> 1);
-          const int a0 = (c0 + (sl >> 2)) * SP + p0 + 4 * (sl & 3);
-          const uint4 v = lds_tr_pair(scr, a0, a0 + 4 * SP);
-          const int col = colbase + c0;
-          const int pp = p0 + sl;
-          const int h = rh + pp / LW, w = r0w + pp % LW;
-          if (col < a.ncols && h < a.Rh && w < a.Rw) {
-            uint16_t* p = plane + (int64_t)h * sd[3] + (int64_t)w * sd[4] + col;
-            const int nvalid = a.ncols - col < 8 ? a.ncols - col : 8;
-            if (nvalid == 8 && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
-              *reinterpret_cast<uint4*>(p) = v;
-            } else {
-              for (int k = 0; k < nvalid; ++k) p[k] = u4_elem(v, k);
-            }
-          }
-        }
-      } else {
-        for (int e = lane; e < 32 * 32; e += 64) {
-          const int c = e >> 5, pp = e & 31;
-          const int col = colbase + c;
-          const int h = rh + pp / LW, w = r0w + pp % LW;
-          if (col < a.ncols && h < a.Rh && w < a.Rw)
-            plane[(int64_t)col * sd[1] + (int64_t)h * sd[3] + (int64_t)w * sd[4]] = scr[c * SP + pp];
-        }
       }
-      __builtin_amdgcn_wave_barrier();
     }
   }
 }
@@ -237,7 +208,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   constexpr int NITEM = G::HD * HH * NSEG;
   static_assert(SRC != 3 || NITEM <= 512, "one staging item per thread");
   constexpr int NREG = SRC == 3 ? 8 : MAXK;          // uint4 registers per set
-  constexpr int PD = MB * NB <= 2 ? 2 : 1;           // fragment read-ahead (steps)
+  constexpr int PD = MB * NB <= 4 ? 2 : 1;           // fragment read-ahead (steps)
   constexpr int HOOK = 1;                            // step after which the next stage is staged
 
   const int tid = threadIdx.x;
@@ -248,8 +219,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   uint4* act = smem4;              // [2][HPAD]
   uint4* wts = smem4 + 2 * HPAD;   // WF: [nchunks][WFRAG], else [2][WFRAG]
   const int wslots = WF ? a.nchunks * WFRAG : 2 * WFRAG;
-  uint16_t* scr = reinterpret_cast<uint16_t*>(wts + wslots) + wv * (32 * G::SP);
-  float* btab = reinterpret_cast<float*>(reinterpret_cast<char*>(wts + wslots) + G::SCR_BYTES);
+  float* btab = reinterpret_cast<float*>(wts + wslots);  // bias per packed column (16-byte aligned)
   const int nbcol = a.nbt_pad * 32;
 
   // Job assignment.  Workgroups are dealt to the 8 XCDs round-robin; each XCD
@@ -306,12 +276,14 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   }
 
   // Per-job byte offsets of this thread's slots (kOob outside the volume).
-  int soff[MAXK];
+  uint32_t soff[MAXK];  // unsigned: an out-of-volume offset plus a channel offset stays out of range
   int cached_key = -1;
   auto job_offsets = [&](const TapCursor& c) __attribute__((always_inline)) {
-    const int key = ((c.n * a.nbd + c.bd) * a.nbh + c.bh) * a.nbw + c.bw;
-    if (key == cached_key) return;
-    cached_key = key;
+    if (SRC != 3) {  // SRC 3 recomputes (one item): no branch ahead of the loads
+      const int key = ((c.n * a.nbd + c.bd) * a.nbh + c.bh) * a.nbw + c.bw;
+      if (key == cached_key) return;
+      cached_key = key;
+    }
     const int s0d = c.bd * G::TD - a.pd, s0h = c.bh * (G::TH * HR) - a.ph, s0w = c.bw * LW - a.pw;
     if (SRC == 3) {
       const int gd = s0d + (item & 255), gh = s0h + ((item >> 8) & 255), gw = c.bw * LW - 8 + 8 * (item >> 16);
@@ -336,30 +308,39 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 
   // Activation loads of stage `cur` into register set `slot`.  An
   // out-of-volume slot's offset stays past num_records after the channel
-  // offset is added (every in-sample offset is below 1 GiB).
-  auto issue_act = [&](const TapCursor& cur, int slot) __attribute__((always_inline)) {
+  // offset is added (every in-sample offset is below 1 GiB).  The loads are
+  // issued whether or not the stage exists (`live`): a stage past the end
+  // reads with every offset out of range (zeros, no memory access) from
+  // sample 0.  Unconditional loads keep the compiler's load counting exact,
+  // so a commit waits only for its own stage's loads, not for every load in
+  // flight.
+  auto issue_act = [&](const TapCursor& cur, int slot, bool live) __attribute__((always_inline)) {
     job_offsets(cur);
-    const int c0 = cur.chunk * 8;
-    const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (int64_t)cur.n * a.ss[0], a.src_bytes);
-    const int coff = 2 * c0 * ss1;  // uniform
+    const int c0 = live ? cur.chunk * 8 : 0;
+    const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), a.src_bytes);
+    const uint32_t coff = live ? 2u * c0 * ss1 : 0u;  // uniform
+    // Disabled loads get bit 31 set in their offset: past any num_records
+    // (every valid offset is below 1 GiB), by arithmetic rather than a select,
+    // which the compiler would turn into branches around duplicated loads.
+    auto gate = [&](uint32_t off, bool on) { return (int)(off | ((uint32_t)!on << 31)); };
     if constexpr (SRC == 3) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         pfa[slot][e] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, c0 + e < a.Cs ? soff[0] + coff + 2 * e * ss1 : kOob, 0, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, gate(soff[0] + coff + 2u * e * ss1, live && c0 + e < a.Cs), 0, 0));
     } else {
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {
       if (SRC == 1) {
-        pfa[slot][k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, soff[k] + coff, 0, 0));
+        pfa[slot][k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, gate(soff[k] + coff, live), 0, 0));
       } else {
         uint32_t wd[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(
-              src, c0 + 2 * q < a.Cs ? soff[k] + coff + 4 * q * ss1 : kOob, 0, 0);
+              src, gate(soff[k] + coff + 4u * q * ss1, live && c0 + 2 * q < a.Cs), 0, 0);
           const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(
-              src, c0 + 2 * q + 1 < a.Cs ? soff[k] + coff + (4 * q + 2) * ss1 : kOob, 0, 0);
+              src, gate(soff[k] + coff + (4u * q + 2) * ss1, live && c0 + 2 * q + 1 < a.Cs), 0, 0);
           wd[q] = lo | (hi << 16);
         }
         pfa[slot][k] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
@@ -446,10 +427,10 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   const int nstage = myjobs * a.cps;
   TapCursor cc = tap_cursor_at(a, j0);
   TapCursor ca = cc, cw = cc;
-  issue_act(ca, 0);
+  issue_act(ca, 0, true);
   tap_advance(a, ca, nx);
-  if (DIST == 2 && nstage > 1) {
-    issue_act(ca, DIST - 1);
+  if (DIST == 2) {
+    issue_act(ca, DIST - 1, nstage > 1);
     tap_advance(a, ca, nx);
   }
   if (!WF) {
@@ -457,16 +438,12 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
     tap_advance(a, cw, nx);
   }
   commit_act(0, 0);
-  if (nstage > DIST) {
-    issue_act(ca, 0);
-    tap_advance(a, ca, nx);
-  }
+  issue_act(ca, 0, nstage > DIST);
+  tap_advance(a, ca, nx);
   if (!WF) {
     commit_w(0);
-    if (nstage > 1) {
-      issue_w(cw);
-      tap_advance(a, cw, nx);
-    }
+    issue_w(cw);
+    tap_advance(a, cw, nx);
   }
 
   // Stage t (BUF = t % 2): data in buffer BUF; the activations of stage t+1
@@ -495,20 +472,18 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(afr[CUR][mb], bfr[CUR][nb], acc[mb][nb]);
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32<T>(bfr[CUR][nb], afr[CUR][mb], acc[mb][nb]);  // C^T
       if constexpr (S == HOOK) {
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < nstage) commit_act(SN, 1 - BUF);
-        if (t + 1 + DIST < nstage) {
-          issue_act(ca, SN);
-          tap_advance(a, ca, nx);
-        }
+        issue_act(ca, SN, t + 1 + DIST < nstage);
+        tap_advance(a, ca, nx);
         if (!WF) {
+          // Weight loads stay in range for any cursor (chunk < nchunks,
+          // column tile < n_ctiles), so they too are issued unconditionally.
           if (t + 1 < nstage) commit_w(1 - BUF);
-          if (t + 2 < nstage) {
-            issue_w(cw);
-            tap_advance(a, cw, nx);
-          }
+          issue_w(cw);
+          tap_advance(a, cw, nx);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -518,7 +493,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
     static_for(std::make_integer_sequence<int, NSTEP>{}, step);
     if (cc.chunk == (cc.split + 1) * a.cps - 1) {
       if (a.nsplit > 1) store_partial(cc);
-      else tap_epilogue<T, NB, MB, LW>(a, acc, wv, lane, cc, scr, btab, 0);
+      else tap_epilogue<T, NB, MB, LW>(a, acc, wv, lane, cc, btab, 0);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -539,8 +514,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 // and run) and runs the epilogue.
 template <typename T, int NB, int MB, int LW>
 __global__ __launch_bounds__(64) void tap_split_epilogue(const RowArgs a) {
-  __shared__ float btab[6 * 32];
-  __shared__ __attribute__((aligned(16))) uint16_t scr[32 * TapGeom<MB, LW>::SP];
+  __shared__ __attribute__((aligned(16))) float btab[NB * 32];
   constexpr int PW = MB * NB * 16 * 64;
   const int lane = threadIdx.x;
   const int tile = blockIdx.x >> 3, wv = blockIdx.x & 7;
@@ -568,7 +542,7 @@ __global__ __launch_bounds__(64) void tap_split_epilogue(const RowArgs a) {
   }
   __syncthreads();
   const TapCursor ec = tap_cursor_at(a, tile * a.nsplit);
-  tap_epilogue<T, NB, MB, LW>(a, acc, wv, lane, ec, scr, btab, ct * NB * 32);
+  tap_epilogue<T, NB, MB, LW>(a, acc, wv, lane, ec, btab, ct * NB * 32);
 }
 
 template <typename T, int NB, int MB, int SRC, int WF, int LW>

@@ -254,7 +254,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   // Loads of one box into the staging registers.  A box whose tile lies
   // inside the volume (the common case) takes the precomputed validity; one
   // on an edge checks every item's position (branch-free).
-  auto issue = [&](const BoxCur& cur) __attribute__((always_inline)) {
+  // The loads are issued whether or not box `cur` exists (`live`): a box past
+  // the end reads with every offset out of range (zeros, no memory access)
+  // from sample 0, which keeps the compiler's load counting exact (a commit
+  // then waits only for its own box's loads).
+  // A disabled load gets bit 31 set in its offset: past any num_records (every
+  // valid offset is below 1 GiB; an edge item's offset may be negative, which
+  // is past it too), by arithmetic rather than a select, which the compiler
+  // would turn into branches around duplicated loads.
+  auto gate = [&](int off, bool on) { return (int)((uint32_t)off | ((uint32_t)!on << 31)); };
+  auto issue = [&](const BoxCur& cur, bool live) __attribute__((always_inline)) {
     const int r0d = cur.bd * Geo::TD, r0h = cur.bh * TH, r0w = cur.bw * 16;
     int s0d, s0h, s0w;
     if (MODE == MODE_T2DW) {
@@ -266,8 +275,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       s0h = r0h - a.ph;
       s0w = r0w - a.pw;
     }
-    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (int64_t)cur.n * a.fs[0], a.f_bytes);
-    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (int64_t)cur.n * a.gs[0], a.g_bytes);
+    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (live ? (int64_t)cur.n * a.fs[0] : 0), a.f_bytes);
+    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (live ? (int64_t)cur.n * a.gs[0] : 0), a.g_bytes);
     const int fbase = 2 * (r0d * fs2 + r0h * fs3 + r0w * fs4);
     const int gbase = 2 * (s0d * gs2 + s0h * gs3 + s0w * gs4);
     const bool f_in = r0d + Geo::TD <= a.Rd && r0h + TH <= a.Rh && r0w + 16 <= a.Rw;
@@ -276,25 +285,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int k = 0; k < NFI; ++k) {
       const int c = fcode[k];
-      bool ok = fval[k];
-      if (!f_in) {
-        const int gd = r0d + (c & 255), gh = r0h + ((c >> 8) & 255), gw = r0w + ((c >> 16) & 255);
-        ok = ok & (gd < a.Rd) & (gh < a.Rh) & (gw < a.Rw);
-      }
+      const int gd = r0d + (c & 255), gh = r0h + ((c >> 8) & 255), gw = r0w + ((c >> 16) & 255);
+      const bool ok = live & fval[k] & (f_in | ((gd < a.Rd) & (gh < a.Rh) & (gw < a.Rw)));
       const int off = fbase + frel[k];
-      if (FL >= 1) pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, ok ? off : kOob, 0, 0));
+      if (FL >= 1) pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, gate(off, ok), 0, 0));
       else pf[k] = load8(fsrc, ok, off, fcv[k], fs1);
     }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
       const int c = gcode[k];
-      bool ok = gval[k];
-      if (!g_in) {
-        const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = s0w + ((c >> 16) & 255);
-        ok = ok & ((unsigned)gd < (unsigned)a.Gd) & ((unsigned)gh < (unsigned)a.Gh) & ((unsigned)gw < (unsigned)a.Gw);
-      }
+      const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = s0w + ((c >> 16) & 255);
+      const bool ok = live & gval[k] &
+                      (g_in | (((unsigned)gd < (unsigned)a.Gd) & ((unsigned)gh < (unsigned)a.Gh) & ((unsigned)gw < (unsigned)a.Gw)));
       const int off = gbase + grel[k];
-      if (FL == 2) pg[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, ok ? off : kOob, 0, 0));
+      if (FL == 2) pg[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, gate(off, ok), 0, 0));
       else pg[k] = load8(gsrc, ok, off, gcv[k], gs1);
     }
   };
@@ -341,13 +345,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const int nbx = box_begin < gb1 ? (gb1 - box_begin + s8 - 1) / s8 : 0;
   BoxCur ca = box_at(box_begin < gb1 ? box_begin : 0);
   if (nbx > 0) {
-    issue(ca);
+    issue(ca, true);
     box_advance(ca);
     commit(0);
-    if (nbx > 1) {
-      issue(ca);
-      box_advance(ca);
-    }
+    issue(ca, nbx > 1);
+    box_advance(ca);
   }
   constexpr int HOOK = 1;
   // K loop of one box with NV column blocks and, with DBF, the bias MFMA.
@@ -381,10 +383,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       if constexpr (ST == HOOK) {
         __builtin_amdgcn_sched_barrier(0);
         if (i + 1 < nbx) commit(BUF ^ 1);
-        if (i + 2 < nbx) {
-          issue(ca);
-          box_advance(ca);
-        }
+        issue(ca, i + 2 < nbx);
+        box_advance(ca);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -417,10 +417,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       }
       if (st == HOOK) {
         if (i + 1 < nbx) commit(BUF ^ 1);
-        if (i + 2 < nbx) {
-          issue(ca);
-          box_advance(ca);
-        }
+        issue(ca, i + 2 < nbx);
+        box_advance(ca);
       }
     }
   };
