@@ -747,11 +747,20 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
       a.fs[3] = a.gs[3] = 16;
     }
   }
+  // k=3 with G w-contiguous too (both NCDHW): G is staged straight from its
+  // source with a register transpose (fl 3) instead of being copied to NDHWC.
+  // Its 8-aligned w segments [r0w - 8, r0w + 24) cover the halo row for pw <= 6.
+  // It loads 1.8x the bytes of NDHWC staging plus the transposes, which costs
+  // more than the copy saves above 64 G channels (measured: 24 and 48 channels
+  // gain 52 and 22 us per trunk pass, 96 loses 15, 192 breaks even).
+  if (p.fl == 1 && p.mode == MODE_K3 && a.Gc <= 64 && a.gs[4] == 1 && a.Gw % 8 == 0 && a.gs[0] % 8 == 0 &&
+      a.gs[1] % 8 == 0 && a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0 && a.pw >= 0 && a.pw <= 6)
+    p.fl = 3;
   if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
     p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
     channels_last_strides(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
   }
-  if (copy_ok && ncdhw_copyable(a.gs, a.Gc, a.Gd, a.Gh, a.Gw)) {
+  if (copy_ok && p.fl != 3 && ncdhw_copyable(a.gs, a.Gc, a.Gd, a.Gh, a.Gw)) {
     p.gcopy_bytes = align256(tensor_bytes(d->n, a.Gc, a.Gd, a.Gh, a.Gw));
     channels_last_strides(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   }
@@ -775,6 +784,7 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   if (p.mode == MODE_K3) TD = WgGeom<MODE_K3>::TD, TH = WgGeom<MODE_K3>::TH, lds = WgGeom<MODE_K3>::LDS_BYTES;
   else if (p.mode == MODE_K1) TD = WgGeom<MODE_K1>::TD, TH = WgGeom<MODE_K1>::TH, lds = WgGeom<MODE_K1>::LDS_BYTES;
   else TD = WgGeom<MODE_T2DW>::TD, TH = WgGeom<MODE_T2DW>::TH, lds = WgGeom<MODE_T2DW>::LDS_BYTES;
+  if (p.fl == 3) lds += WgGeom<MODE_K3>::TRASH_BYTES;
   a.nbd = cdiv(a.Rd, TD);
   a.nbh = cdiv(a.Rh, TH);
   a.nbw = cdiv(a.Rw, 16);
@@ -839,9 +849,15 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   // loads per slot.
   const bool f16b = (reinterpret_cast<uintptr_t>(a.fsrc) & 15) == 0;
   const bool g16b = (reinterpret_cast<uintptr_t>(a.gsrc) & 15) == 0;
-  const int fl = (p.fl == 2 && f16b && g16b) ? 2 : ((p.fl && f16b) ? 1 : 0);
+  // fl 3 needs both sources 16-byte aligned; otherwise G falls back to scalar
+  // staging (correct for any strides, slower).
+  const int fl = (p.fl == 3 && f16b && g16b) ? 3 : (p.fl == 2 && f16b && g16b) ? 2 : ((p.fl && f16b) ? 1 : 0);
   const bool g_ok = vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0;
-  const int cl = fl == 2 ? 1 : ((g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0);
+  const int cl = fl == 3 ? 0 : fl == 2 ? 1 : ((g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0);
+  // fl 3 stages 18 * GCW G items per box: one per thread, plus 64 more in one
+  // wave when CBW = 4.
+  if (fl == 3 && 18 * a.GCW > WgGeom<MODE_K3>::THREADS + (p.cbw == 4 ? 64 : 0))
+    return fail(R3C_INVALID, "internal: %d G staging items exceed the kernel's capacity", 18 * a.GCW);
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
   TimedLaunch tl(KIND_WGRAD, s);
   const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, fl, a, p.lds, s);

@@ -82,6 +82,7 @@ struct WgGeom {
   // channel-major [32 channels][FP positions] like F.
   static constexpr int GT = HPOS * 32 > 32 * FP ? HPOS * 32 : 32 * FP;
   static constexpr int LDS_BYTES = 2 * (FT + GT) * 2;                 // double-buffered tiles
+  static constexpr int TRASH_BYTES = THREADS * 16;                    // k=3 NCDHW G staging: one slot per thread
 };
 
 struct WgArgs {

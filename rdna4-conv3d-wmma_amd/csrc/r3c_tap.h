@@ -99,9 +99,30 @@ __device__ __forceinline__ TapCursor tap_cursor_at(const RowArgs& a, int job) {
 }
 
 // Next stage: the next chunk of the job, else the first chunk of job + stride.
-__device__ __forceinline__ void tap_advance(const RowArgs& a, TapCursor& c, int stride) {
+// `st` holds the stride's digits in the job index's mixed radix (split, column
+// tile, box w, h, d, sample; tap_cursor_at(a, stride)), so moving to the next
+// job is a digit-wise add with carries instead of five divisions.  Each digit
+// sum is below twice its radix, so one conditional subtraction normalises it.
+__device__ __forceinline__ void tap_advance(const RowArgs& a, TapCursor& c, const TapCursor& st) {
   if (++c.chunk < (c.split + 1) * a.cps) return;
-  c = tap_cursor_at(a, c.job + stride);
+  int v = c.split + st.split;
+  int cy = v >= a.nsplit;
+  c.split = cy ? v - a.nsplit : v;
+  v = c.ct + st.ct + cy;
+  cy = v >= a.n_ctiles;
+  c.ct = cy ? v - a.n_ctiles : v;
+  v = c.bw + st.bw + cy;
+  cy = v >= a.nbw;
+  c.bw = cy ? v - a.nbw : v;
+  v = c.bh + st.bh + cy;
+  cy = v >= a.nbh;
+  c.bh = cy ? v - a.nbh : v;
+  v = c.bd + st.bd + cy;
+  cy = v >= a.nbd;
+  c.bd = cy ? v - a.nbd : v;
+  c.n += st.n + cy;
+  c.chunk = c.split * a.cps;
+  c.job += st.job;
 }
 
 // Output tile (box, column tile) of a cursor.
@@ -426,24 +447,25 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   // stage 1 in flight.
   const int nstage = myjobs * a.cps;
   TapCursor cc = tap_cursor_at(a, j0);
+  const TapCursor stride = tap_cursor_at(a, nx);  // digits of the job stride
   TapCursor ca = cc, cw = cc;
   issue_act(ca, 0, true);
-  tap_advance(a, ca, nx);
+  tap_advance(a, ca, stride);
   if (DIST == 2) {
     issue_act(ca, DIST - 1, nstage > 1);
-    tap_advance(a, ca, nx);
+    tap_advance(a, ca, stride);
   }
   if (!WF) {
     issue_w(cw);
-    tap_advance(a, cw, nx);
+    tap_advance(a, cw, stride);
   }
   commit_act(0, 0);
   issue_act(ca, 0, nstage > DIST);
-  tap_advance(a, ca, nx);
+  tap_advance(a, ca, stride);
   if (!WF) {
     commit_w(0);
     issue_w(cw);
-    tap_advance(a, cw, nx);
+    tap_advance(a, cw, stride);
   }
 
   // Stage t (BUF = t % 2): data in buffer BUF; the activations of stage t+1
@@ -477,13 +499,13 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < nstage) commit_act(SN, 1 - BUF);
         issue_act(ca, SN, t + 1 + DIST < nstage);
-        tap_advance(a, ca, nx);
+        tap_advance(a, ca, stride);
         if (!WF) {
           // Weight loads stay in range for any cursor (chunk < nchunks,
           // column tile < n_ctiles), so they too are issued unconditionally.
           if (t + 1 < nstage) commit_w(1 - BUF);
           issue_w(cw);
-          tap_advance(a, cw, nx);
+          tap_advance(a, cw, stride);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -501,7 +523,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
     }
-    tap_advance(a, cc, nx);
+    tap_advance(a, cc, stride);
   };
   for (int t = 0; t < nstage; t += 2) {
     run_stage(t, std::integral_constant<int, 0>{});

@@ -50,7 +50,12 @@ namespace r3c {
 // positions; its A fragment (8 consecutive positions of one channel) is then a
 // single ds_read_b128, and the padded pitch (FP = BOXPOS + 8) puts the 16
 // lanes of a group on 16 distinct bank slots.  FL 2 (k=1 without padding,
-// where G has no tap shift): G is staged and read the same way.
+// where G has no tap shift): G is staged and read the same way.  FL 3 (k=3, G
+// w-contiguous as well): F as with FL 1; G keeps its [position][channel] halo
+// tile but is staged from the w-contiguous source: an item (halo row,
+// 8-channel group, 8-position segment) loads 8 positions of each of its 8
+// channels with eight 16-byte loads and transposes them in registers into 8
+// slots, so no NDHWC copy of G is needed.
 template <typename T, int MODE, int CBW, int CL, int FL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) void wgrad_kernel(const WgArgs a) {
   extern __shared__ uint4 smem4[];
@@ -66,10 +71,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   constexpr int TILE = FT + Geo::GT;  // halves per buffer
   constexpr int NDBG = MODE == MODE_T2DW ? CBW : 1;
   constexpr int WS = MODE == MODE_T2DW ? 2 : 1;  // G positions per F position along each axis
+  // FL 3 G items per thread: HD * HH * 4 * GCW / 8 = 18 GCW items, one per
+  // thread up to GCW = 24 (CBW <= 3); at GCW = 32 (CBW = 4) the 64 items past
+  // the first 512 go to wave XW, which owns three of the 27 column blocks
+  // (waves 0-2 own four, wave 7 adds the bias MFMA).
+  constexpr int NGW = FL == 3 ? (CBW == 4 ? 2 : 1) : 1;
+  constexpr int XW = 6;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);  // the same, known wave-uniform
   const int g = lane >> 5;          // MFMA k half (positions 8g .. 8g+7 of a step)
   const int h = (lane >> 4) & 1;    // which 16-lane half of the 32 columns / rows
   const int s = lane & 15;          // lane inside its 16-lane group
@@ -172,6 +184,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const int gs1 = (int)a.gs[1], gs2 = (int)a.gs[2], gs3 = (int)a.gs[3], gs4 = (int)a.gs[4];
 
   u32x4_t pf[NFI], pg[NGI];
+  u32x4_t pgw[NGW][8];  // FL 3: eight channels x 8 positions per G item
   auto load8 = [&](const __amdgpu_buffer_rsrc_t& rs, bool ok, int off, int cvalid, int cs1) -> u32x4_t {
     if (CL) return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : kOob, 0, 0));
     u32x4_t v;
@@ -219,6 +232,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       grel[k] = 2 * (hd * gs2 + hh * gs3 + hw * gs4 + c0 * gs1);
       gval[k] = c >= 0 && c0 < a.Gc;
       gcv[k] = a.Gc - c0;
+    }
+  }
+  // FL 3 G items: item it = NT k + tid is (halo row, channel group cg,
+  // segment j), j fastest so four neighbouring lanes load one 64-byte run.
+  // Segment j covers w in [r0w - 8 + 8j, r0w + 8j) (r0w = the box's first w,
+  // a multiple of 16; W % 8 == 0, so a segment is wholly inside or outside the
+  // volume), i.e. tile columns hw0 = pw - 8 + 8j .. hw0 + 7, of which those in
+  // [0, HW) are written (gwmask).  Code (hd, hh, j, cg), 8 bits each.
+  static_assert(FL != 3 || (MODE == MODE_K3 && Geo::HD * HH * 4 * (CBW == 4 ? 4 : 3) <= NT + (NGW - 1) * 64),
+                "FL 3: G items per thread");
+  int gwcode[NGW], gwrel[NGW], gwmask[NGW], gwslot[NGW];
+  if (FL == 3) {
+    const int ncg = a.GCW >> 3;
+#pragma unroll
+    for (int k = 0; k < NGW; ++k) {
+      const int it = k == 0 ? tid : (wv == XW ? NT + lane : 1 << 20);
+      const int j = it & 3, rest = it >> 2;
+      const int cg = rest % ncg, row = rest / ncg;
+      const int hd = row / HH, hh = row - (row / HH) * HH;
+      const bool ex = row < Geo::HD * HH;  // false for k = 1 outside wave XW
+      const int hw0 = a.pw - 8 + 8 * j;
+      int m = 0;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) m |= ((unsigned)(hw0 + p) < (unsigned)HW) ? (1 << p) : 0;
+      gwcode[k] = ex ? (hd | (hh << 8) | (j << 16) | (cg << 24)) : -1;
+      gwmask[k] = ex ? m : 0;
+      gwslot[k] = ((hd * HH + hh) * HW + hw0) * 32 + cg * 8;  // halves; only masked columns are written
+      gwrel[k] = 2 * (hd * gs2 + hh * gs3 + 8 * j - 8 + (gc0 + cg * 8) * gs1);
     }
   }
 
@@ -291,6 +332,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       if (FL >= 1) pf[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(fsrc, gate(off, ok), 0, 0));
       else pf[k] = load8(fsrc, ok, off, fcv[k], fs1);
     }
+    if constexpr (FL == 3) {
+      // Tile rows start at (s0d, s0h); segments are addressed from the box's first w.
+      const int gb3 = 2 * (s0d * gs2 + s0h * gs3 + r0w);
+#pragma unroll
+      for (int k = 0; k < NGW; ++k) {
+        if (k > 0 && wvu != XW) break;  // wave-uniform: only wave XW holds second items
+        const int c = gwcode[k];
+        const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = r0w - 8 + 8 * ((c >> 16) & 255);
+        const int ch0 = gc0 + 8 * ((c >> 24) & 255);
+        const bool ok = live & (c >= 0) & ((unsigned)gd < (unsigned)a.Gd) & ((unsigned)gh < (unsigned)a.Gh) &
+                        ((unsigned)gw < (unsigned)a.Gw);
+        const int off = gb3 + gwrel[k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pgw[k][e] = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, gate(off + 2 * e * gs1, ok & (ch0 + e < a.Gc)), 0, 0));
+      }
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
       const int c = gcode[k];
@@ -313,6 +373,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         if (FL >= 1) *reinterpret_cast<u32x4_t*>(ft + (c >> 24) * FP + pos) = pf[k];
         else *reinterpret_cast<u32x4_t*>(ft + pos * 32 + (c >> 24) * 8) = pf[k];
       }
+    }
+    if constexpr (FL == 3) {
+      // Position p of channel e is half p of pgw[k][e]; slot p gathers the
+      // eight channels of position p (v_perm picks the 16-bit halves).  A
+      // position outside the tile row is written to this thread's trash slot
+      // (past both buffers) instead of being branched around.
+      uint16_t* const trash = tiles + 2 * TILE + tid * 8;
+#pragma unroll
+      for (int k = 0; k < NGW; ++k) {
+        if (k > 0 && wvu != XW) break;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const uint32_t sel = (p & 1) ? 0x07060302u : 0x05040100u;
+          u32x4_t v;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = __builtin_amdgcn_perm(pgw[k][2 * q + 1][p >> 1], pgw[k][2 * q][p >> 1], sel);
+          uint16_t* const dst = (gwmask[k] & (1 << p)) ? gtl + gwslot[k] + p * 32 : trash;
+          *reinterpret_cast<u32x4_t*>(dst) = v;
+        }
+      }
+      return;
     }
 #pragma unroll
     for (int k = 0; k < NGI; ++k) {
