@@ -21,7 +21,8 @@ Also reported on the same JSON line:
                 (these also pick the dominant kernel).
   hbm_passes    BASELINE configs 3 and 4 (k=1 fp16, ConvTranspose3d k2s2 bf16):
                 per-pass time (all kernels of the pass, median of 20, MALL
-                flushed before each) and compulsory HBM bytes / time vs 8 TB/s.
+                flushed before each by a 512 MB write and a 512 MB read) and
+                compulsory HBM bytes / time vs 8 TB/s.
   cpu_baseline  the reference's CPU path (Conv3dWmma on CPU tensors ->
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
@@ -58,7 +59,7 @@ PASSES = ("fwd", "dx", "dw")
 # memory-bound passes, judged on compulsory HBM bytes per pass.
 POINTWISE = [(4, 48, 24, 64, 128, 128), (4, 24, 96, 64, 128, 128)]   # (N, Cin, Cout, D, H, W)
 CONVT = [(4, 192, 96, 8, 16, 16), (4, 48, 24, 32, 64, 64)]           # (N, Cin, Cout, D, H, W) of the input
-FLUSH_BYTES = 512 << 20  # written between repetitions so no pass reads its operands from the 256 MB MALL
+FLUSH_BYTES = 512 << 20  # written, then another buffer of this size read, between repetitions (256 MB MALL)
 
 
 def _flops(n, ci, co, d, h, w):
@@ -204,12 +205,16 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup):
 def hbm_passes(layout: str, reps: int = 20):
     """BASELINE configs 3 and 4: per-pass time (median over reps of the summed
     kernel durations of the pass, HIP events on the launch stream) and the
-    compulsory HBM bytes over that time.  A 512 MB buffer is written before
-    every repetition, so small working sets are not served from the MALL."""
+    compulsory HBM bytes over that time.  Before every repetition a 512 MB
+    buffer is written and a second 512 MB buffer is read: the write evicts the
+    working set from the 256 MB MALL, the read leaves the MALL holding clean
+    lines, so the timed pass neither hits its operands there nor pays for
+    writing back an unrelated kernel's dirty lines."""
     import torch
     from rdna4_conv3d import _native as nat
     dev = torch.device("cuda", 0)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    flush_rd = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
 
     def L(t):
         return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
@@ -223,6 +228,7 @@ def hbm_passes(layout: str, reps: int = 20):
         tot = []
         for r in range(reps):
             flush.zero_()
+            flush_rd.sum()
             nat.timing_enable(True)
             nat.timing_collect()
             fn()
@@ -269,7 +275,7 @@ def hbm_passes(layout: str, reps: int = 20):
                 "us": round(ms * 1e3, 2), "bytes": by, "gbs": round(by / (ms * 1e-3) / 1e9, 1),
                 "frac_hbm": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del x, go, y, dw, db
-    del flush
+    del flush, flush_rd
     torch.cuda.empty_cache()
     return out
 

@@ -688,12 +688,100 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // ---------------------------------------------------------------------------
 struct WgPlan {
   int mode, cbw, taps, ngroups;
+  int pw;              // 1: register-direct single-tap kernel (r3c_pwdw.h), fields below
+  int tr, tc, nj;
+  PwdwArgs pa;
   int fl;  // 1: F staged channel-major from its w-contiguous source; 2: G too (k=1, no padding)
   WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
   int64_t fcopy_bytes, gcopy_bytes;  // > 0: that operand is first copied to NDHWC
 };
+
+// Dense w-contiguous planes (NCDHW-like: channel and sample strides free).
+bool dense_planes(const int64_t* st, int64_t h, int64_t w) {
+  return st[4] == 1 && st[3] == w && st[2] == h * w && st[1] % 8 == 0 && st[0] % 8 == 0 && st[0] > 0 && st[1] > 0;
+}
+
+// Register-direct plan for the single-tap weight gradients (Conv3d k=1 without
+// padding, ConvTranspose k2s2) when both operands have dense w-contiguous
+// planes: K blocks of 64 positions (k=1, S % 64 == 0) or of 16 / 32 positions
+// within one w row (ConvTranspose, W % 16 == 0).  The GEMM always reserves the
+// bias gradient's ones row / column, so the plan does not depend on db.
+bool plan_pwdw(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
+  WgArgs& w = p.a;
+  PwdwArgs& a = p.pa;
+  memset(&a, 0, sizeof a);
+  int64_t S;
+  if (transpose) {
+    if (!dense_planes(w.fs, w.Rh, w.Rw) || !dense_planes(w.gs, 2ll * w.Rh, 2ll * w.Rw)) return false;
+    if (w.Gd != 2 * w.Rd || w.Gh != 2 * w.Rh || w.Gw != 2 * w.Rw || w.Rw % 16 != 0) return false;
+    p.nj = w.Rw % 32 == 0 ? 2 : 1;
+    S = (int64_t)w.Rd * w.Rh * w.Rw;
+  } else {
+    // k=1: with at most 32 output channels (one row block) the LDS-staged
+    // kernel streams faster (measured 168 vs 196 us at [4,48,64,128,128] -> 24;
+    // 338 vs 404 us the other way at -> 96).
+    if (d->kernel != 1 || w.pd || w.ph || w.pw || w.Fc <= 32) return false;
+    if (!dense_planes(w.fs, w.Rh, w.Rw) || !dense_planes(w.gs, w.Gh, w.Gw)) return false;
+    if (w.Gd != w.Rd || w.Gh != w.Rh || w.Gw != w.Rw) return false;
+    p.nj = 4;
+    S = (int64_t)w.Rd * w.Rh * w.Rw;
+    if (S % 64 != 0) return false;
+  }
+  if (S * d->n >= (1ll << 31)) return false;
+  a.f_bytes = sample_bytes(w.fs, w.Fc, w.Rd, w.Rh, w.Rw);
+  a.g_bytes = sample_bytes(w.gs, w.Gc, w.Gd, w.Gh, w.Gw);
+  if (a.f_bytes == 0 || a.g_bytes == 0) return false;
+  a.fs0 = w.fs[0];
+  a.fs1 = w.fs[1];
+  a.gs0 = w.gs[0];
+  a.gs1 = w.gs[1];
+  a.Fc = w.Fc;
+  a.Gc = w.Gc;
+  a.taps = p.taps;
+  a.S = (int32_t)S;
+  a.W = w.Rw;
+  a.HW = w.Rh * w.Rw;
+  a.M = w.Fc + (transpose ? 1 : 0);
+  a.ncols = p.taps * w.Gc + (transpose ? 0 : 1);
+  // Tiles per workgroup (TR x TC blocks of 32): the instantiated shapes that
+  // fit the register file -- TR * TC <= 3 for k=1 (64-position K blocks), and
+  // up to 2 x 2 for ConvTranspose.
+  const int nrb = cdiv(a.M, 32), ncb = cdiv(a.ncols, 32);
+  if (transpose) {
+    p.tr = std::min(nrb, 2);
+    p.tc = std::min(ncb, p.tr == 1 ? 3 : 2);
+    if (nrb >= 3 && ncb == 1) p.tr = 3;
+  } else {
+    p.tr = std::min(nrb, 3);
+    p.tc = std::min(ncb, 3 / p.tr);
+  }
+  a.ngr = cdiv(nrb, p.tr);
+  a.ngc = cdiv(ncb, p.tc);
+  const int kbpos = 16 * p.nj;
+  a.nkb = (int32_t)(S * d->n / kbpos);
+  // About two workgroups per CU, at least 8 K blocks (one per wave) each, and
+  // at most kMaxPartialBytes of partials.
+  const int ntg = a.ngr * a.ngc;
+  const int64_t per_split = (int64_t)w.Fc * p.taps * w.Gc * 4;
+  int64_t nsplit = cdiv((int64_t)2 * kNumCUs, ntg);
+  nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, a.nkb / 8));
+  nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
+  if (nsplit >= 8) nsplit -= nsplit % 8;  // a grid of whole XCD eighths (the kernel's renumbering)
+  a.nsplit = (int32_t)std::max<int64_t>(1, nsplit);
+  a.kil = transpose ? 1 : 0;  // K-block order per split (measured per mode)
+  p.pw = 1;
+  p.mode = transpose ? MODE_T2DW : MODE_K1;
+  p.part_bytes = align256(a.nsplit * per_split);
+  p.dbpart_bytes = align256((int64_t)a.nsplit * std::max(w.Fc, 8 * w.Gc) * 4);
+  p.ngroups = cdiv(a.nsplit, kReduceGroup);
+  p.nelem = (int64_t)w.Fc * p.taps * w.Gc + std::max(w.Fc, w.Gc);
+  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
+  p.fcopy_bytes = p.gcopy_bytes = 0;
+  p.lds = 0;
+  return true;
+}
 
 void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   WgArgs& a = p.a;
@@ -716,6 +804,8 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
     memcpy(a.fs, d->y_strides, sizeof a.fs);
     memcpy(a.gs, d->x_strides, sizeof a.gs);
   }
+  p.pw = 0;
+  if (plan_pwdw(d, transpose, p)) return;
   // NCDHW operands of the k=3 pass are copied to NDHWC first: the tiles are
   // [position][channel], which strided staging fills slowly, and the pass does
   // enough arithmetic per byte to pay for the copy.  The memory-bound k=1 and
@@ -809,12 +899,55 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
 }
 
+// Register-direct single-tap weight gradient, then the shared fixed-order reduce.
+int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void* x, const void* dy, void* dw,
+             int dw_dtype, void* db, int db_dtype, void* ws, hipStream_t s) {
+  PwdwArgs a = p.pa;
+  a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
+  a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
+  if ((reinterpret_cast<uintptr_t>(a.fsrc) | reinterpret_cast<uintptr_t>(a.gsrc)) & 15)
+    return fail(R3C_UNSUPPORTED, "single-tap weight gradient needs 16-byte aligned tensors");
+  a.part = static_cast<float*>(ws);
+  a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
+  a.db_mode = db ? (transpose ? 2 : 1) : 0;
+  TimedLaunch tl(KIND_WGRAD, s);
+  const bool launched = launch_pwdw(d->dtype, p.mode, p.tr, p.tc, p.nj, a, s);
+  tl.end();
+  if (!launched)
+    return fail(R3C_UNSUPPORTED, "no single-tap weight-gradient instantiation for tiles %dx%d nj %d", p.tr, p.tc, p.nj);
+  int rc = check_launch("single-tap weight-gradient kernel");
+  if (rc) return rc;
+  ReduceArgs r;
+  memset(&r, 0, sizeof r);
+  r.part = a.part;
+  r.dbpart = a.dbpart;
+  r.dw = dw;
+  r.db = db;
+  r.nsplit = a.nsplit;
+  r.Fc = a.Fc;
+  r.Gc = a.Gc;
+  r.taps = p.taps;
+  r.Fpad = a.Fc;
+  r.Gpad = a.Gc;
+  r.dw_dtype = dw_dtype;
+  r.db_dtype = db_dtype;
+  r.db_mode = a.db_mode;
+  r.ngroups = p.ngroups;
+  r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
+  {
+    TimedLaunch tr(KIND_REDUCE, s);
+    launch_wgrad_reduce(r, s);
+    tr.end();
+  }
+  return check_launch("weight-gradient reduce");
+}
+
 int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void* dy, void* dw, int dw_dtype, void* db,
               int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
   WgPlan p;
   plan_wgrad(d, transpose, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
-  if (p.a.f_bytes == 0 || p.a.g_bytes == 0)
+  if (!p.pw && (p.a.f_bytes == 0 || p.a.g_bytes == 0))  // the register-direct plan checks its own
     return fail(R3C_UNSUPPORTED, "one sample exceeds 1 GiB (32-bit buffer offsets)");
   const int64_t need = p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
   if (ws_bytes < need)
@@ -826,6 +959,7 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   int rc = check_device();
   if (rc) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (p.pw) return run_pwdw(d, transpose, p, x, dy, dw, dw_dtype, db, db_dtype, ws, s);
   WgArgs a = p.a;
   a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);

@@ -105,6 +105,27 @@ struct WgArgs {
   int32_t nblocks;
 };
 
+// Register-direct weight gradient of the single-tap passes (Conv3d k=1
+// unpadded, ConvTranspose k2s2) on w-contiguous dense operands: r3c_pwdw.h.
+struct PwdwArgs {
+  const uint16_t* fsrc;   // F rows: dY (k=1) or x (ConvTranspose), [N][Fc][S] planes dense
+  const uint16_t* gsrc;   // G columns: x (k=1) or dY (ConvTranspose, grid 2D x 2H x 2W)
+  float* part;            // [nsplit][Fc][taps][Gc] fp32 partials
+  float* dbpart;          // db_mode 1: [nsplit][Fc]; 2: [nsplit][8][Gc]
+  int64_t fs0, fs1;       // F sample / channel strides (elements)
+  int64_t gs0, gs1;       // G sample / channel strides
+  uint32_t f_bytes, g_bytes;  // per-sample buffer ranges
+  int32_t Fc, Gc, taps;
+  int32_t S;              // F-grid positions per sample
+  int32_t W, HW;          // ConvTranspose: F-grid w extent and h*w extent
+  int32_t M, ncols;       // GEMM rows (Fc, +1 ones row for db_mode 2), columns (taps*Gc, +1 ones column for db_mode 1)
+  int32_t ngr, ngc;       // tile groups along rows / columns
+  int32_t nkb;            // K blocks (16 NJ positions) over N * S
+  int32_t nsplit;         // K splits (workgroups per tile group)
+  int32_t db_mode;        // 0 none, 1 db = row sums of F, 2 db = column sums of G
+  int32_t kil;            // 1: K blocks interleaved over the splits; 0: contiguous range per split
+};
+
 struct ReduceArgs {
   const float* part;
   const float* dbpart;
@@ -153,5 +174,8 @@ void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
 // One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
+// Register-direct single-tap weight gradient (mode MODE_K1 with nj 4, or
+// MODE_T2DW with nj 1 / 2); false if no instantiation matches.
+bool launch_pwdw(int dtype, int mode, int tr, int tc, int nj, const PwdwArgs& a, hipStream_t stream);
 
 }  // namespace r3c

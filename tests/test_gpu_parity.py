@@ -65,6 +65,10 @@ CONV_CASES = [
     (2, 24, 24, 16, 64, 64, 3, 1),   # more tiles than CUs: multi-job workgroups, no split K
     (2, 20, 24, 18, 70, 40, 3, 1),   # the same with ragged channels and box edges
     (2, 1, 24, 16, 64, 64, 3, 1),    # one source channel (the first UNet layer)
+    # k=1 unpadded with D*H*W % 64 == 0 (NCDHW: register-direct dW when Cout > 32):
+    # 2 x 1 tile groups over two column groups, a 3 x 1 tile group
+    (2, 96, 40, 4, 4, 32, 1, 0),
+    (2, 24, 96, 2, 8, 32, 1, 0),
 ]
 
 
@@ -112,6 +116,10 @@ CONVT_CASES = [
     (1, 192, 96, 2, 4, 16),
     (1, 5, 3, 2, 2, 3),
     (2, 40, 24, 3, 5, 40),   # w % 8 == 0 with a ragged second line and a ragged channel chunk (NCDHW: channel-major staging)
+    # NCDHW register-direct dW (w % 16 == 0): 32-position K blocks (w % 32 == 0)
+    # over four column tile groups; a 3 x 1 tile group (Cout * 8 <= 32)
+    (1, 24, 40, 2, 3, 64),
+    (1, 70, 4, 2, 2, 32),
 ]
 
 
@@ -158,6 +166,7 @@ def test_convt_native_parity(case, layout, dtype):
 DETERMINISM_CASES = [
     (1, 192, 192, 4, 8, 16, 3, 1),   # row kernel split K (fwd and dX)
     (2, 24, 24, 16, 32, 32, 3, 1),   # NCDHW copy path; dW with two-level reduce
+    (2, 24, 48, 8, 16, 32, 1, 0),    # k=1: register-direct dW (NCDHW) with a two-level reduce
 ]
 
 
