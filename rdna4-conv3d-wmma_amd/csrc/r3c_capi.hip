@@ -612,8 +612,99 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   p.part_bytes = split > 1 ? align256(p.ntiles * split * 4 * mb * p.nb * 16 * 64 * 4) : 0;
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct ConvTranspose dX (r3c_t2dx.h)
+// ---------------------------------------------------------------------------
+struct T2dxPlan {
+  int rb;
+  T2dxArgs a;
+  T2dxPackArgs pk;
+  size_t lds;
+  int64_t wpk_bytes;
+};
+
+// w-contiguous dY with even strides (4-byte pair loads), dX with dense planes
+// (positions addressed directly), S % 32 == 0 and N * S < 2^31.
+bool plan_t2dx(const r3c_conv_desc* d, T2dxPlan& p) {
+  memset(&p, 0, sizeof p);
+  T2dxArgs& a = p.a;
+  const int64_t* ys = d->y_strides;
+  const int64_t* xs = d->x_strides;
+  const int64_t D = d->d, H = d->h, W = d->w;
+  if (ys[4] != 1 || ys[3] % 2 || ys[2] % 2 || ys[1] % 2 || ys[0] % 2) return false;
+  if (xs[4] != 1 || xs[3] != W || xs[2] != H * W || xs[1] <= 0 || xs[0] <= 0) return false;
+  const int64_t S = D * H * W;
+  if (S % 32 != 0 || S * d->n >= (1ll << 31)) return false;
+  a.dy_bytes = sample_bytes(ys, d->cout, 2 * D, 2 * H, 2 * W);
+  a.dx_bytes = sample_bytes(xs, d->cin, D, H, W);
+  if (a.dy_bytes == 0 || a.dx_bytes == 0) return false;
+  a.ys0 = ys[0];
+  a.ys1 = ys[1];
+  a.ys2 = (int32_t)ys[2];
+  a.ys3 = (int32_t)ys[3];
+  a.xs0 = xs[0];
+  a.xs1 = xs[1];
+  a.Cin = d->cin;
+  a.Cout = d->cout;
+  a.nks = cdiv(8 * d->cout, 16);
+  if (a.nks > 64) return false;  // A fragments of a row block beyond 64 KB of LDS
+  // Two row blocks per workgroup where they fit 64 KB of LDS (more spill).
+  const int nrb = cdiv(d->cin, 32);
+  const int rb = (nrb >= 2 && 2 * a.nks <= 64) ? 2 : 1;
+  a.nrg = cdiv(nrb, rb);
+  p.rb = cdiv(nrb, a.nrg);
+  a.S = (int32_t)S;
+  a.W = (int32_t)W;
+  a.HW = (int32_t)(H * W);
+  a.ncb = (int32_t)(S * d->n / 32);
+  // About two workgroups per CU over all row groups, each wave with at least
+  // one column block.
+  a.ncw = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv((int64_t)a.ncb, 8), cdiv((int64_t)2 * kNumCUs, a.nrg)));
+  p.lds = (size_t)p.rb * a.nks * 1024;
+  p.pk.cin = d->cin;
+  p.pk.cout = d->cout;
+  p.pk.nks = a.nks;
+  p.pk.total = a.nrg * p.rb * a.nks * 64;
+  p.wpk_bytes = (int64_t)p.pk.total * 16;
+  return true;
+}
+
+int run_t2dx(const r3c_conv_desc* d, const T2dxPlan& p, const void* dy, const void* w, void* dx, void* ws,
+             int64_t ws_bytes, hipStream_t s) {
+  if (ws_bytes < p.wpk_bytes)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)p.wpk_bytes);
+  if (!dy || !w || !dx || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dx)) & 3)
+    return fail(R3C_UNSUPPORTED, "ConvTranspose dX needs 4-byte aligned tensors");
+  int rc = check_device();
+  if (rc) return rc;
+  T2dxPackArgs pk = p.pk;
+  pk.w = static_cast<const uint16_t*>(w);
+  pk.out = static_cast<uint16_t*>(ws);
+  {
+    TimedLaunch tl(KIND_PACK, s);
+    launch_t2dx_pack(pk, s);
+    tl.end();
+  }
+  rc = check_launch("ConvTranspose dX weight pack");
+  if (rc) return rc;
+  T2dxArgs a = p.a;
+  a.dy = static_cast<const uint16_t*>(dy);
+  a.apk = static_cast<const uint16_t*>(ws);
+  a.dx = static_cast<uint16_t*>(dx);
+  TimedLaunch tl(KIND_ROW, s);
+  const bool launched = launch_t2dx(d->dtype, p.rb, a, p.lds, s);
+  tl.end();
+  if (!launched) return fail(R3C_UNSUPPORTED, "no ConvTranspose dX instantiation for rb %d", p.rb);
+  return check_launch("ConvTranspose dX kernel");
+}
+
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
             int64_t ws_bytes, void* stream) {
+  if (op == OP_T2_DX) {
+    T2dxPlan tp;
+    if (plan_t2dx(d, tp)) return run_t2dx(d, tp, src, w, dst, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+  }
   RowPlan p;
   plan_row(d, op, p);
   if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
@@ -1026,6 +1117,10 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
 
 int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
+  if (op == OP_T2_DX) {
+    T2dxPlan tp;
+    if (plan_t2dx(d, tp)) return align256(tp.wpk_bytes);
+  }
   RowPlan p;
   plan_row(d, op, p);
   return align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;

@@ -126,6 +126,29 @@ struct PwdwArgs {
   int32_t kil;            // 1: K blocks interleaved over the splits; 0: contiguous range per split
 };
 
+// Register-direct ConvTranspose k2s2 dX on a w-contiguous dY and a dX with
+// dense planes: r3c_t2dx.h.
+struct T2dxArgs {
+  const uint16_t* dy;
+  const uint16_t* apk;    // A fragments [row group][RB][nks][64 lanes][8]
+  uint16_t* dx;
+  int64_t ys0, ys1;       // dY sample / channel strides (elements)
+  int32_t ys2, ys3;       // dY d / h strides (the w stride is 1)
+  int64_t xs0, xs1;       // dX sample / channel strides (planes dense)
+  uint32_t dy_bytes, dx_bytes;  // per-sample buffer ranges
+  int32_t Cin, Cout;
+  int32_t nks;            // k-steps of 16 over k = 8 Cout
+  int32_t S, W, HW;       // dX positions per sample; its w and h*w extents
+  int32_t ncb;            // column blocks of 32 positions over N * S
+  int32_t nrg, ncw;       // row groups; workgroups per row group
+};
+
+struct T2dxPackArgs {
+  const uint16_t* w;      // ConvTranspose weight (Cin, Cout, 2, 2, 2)
+  uint16_t* out;
+  int32_t cin, cout, nks, total;
+};
+
 struct ReduceArgs {
   const float* part;
   const float* dbpart;
@@ -177,5 +200,8 @@ void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 // Register-direct single-tap weight gradient (mode MODE_K1 with nj 4, or
 // MODE_T2DW with nj 1 / 2); false if no instantiation matches.
 bool launch_pwdw(int dtype, int mode, int tr, int tc, int nj, const PwdwArgs& a, hipStream_t stream);
+// Register-direct ConvTranspose dX (rb 1 or 2 row blocks per workgroup).
+bool launch_t2dx(int dtype, int rb, const T2dxArgs& a, size_t lds, hipStream_t stream);
+void launch_t2dx_pack(const T2dxPackArgs& a, hipStream_t stream);
 
 }  // namespace r3c
