@@ -382,7 +382,7 @@ TapBox tap_box(int mb, int lw) {
   b.HPAD = (b.HPOS + 15) / 16 * 16;
   return b;
 }
-constexpr int64_t kTapScratch = 0;               // the epilogue stores from registers
+constexpr int64_t kTapScratch = 512 * 16;        // one 16-byte trash slot per thread (NCDHW staging)
 constexpr int kTapStep = 14;                      // MFMA steps per 8-channel chunk (27 taps)
 
 // Conv3d k=3 plan on the tap kernel; `a` already holds the source/destination

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   constexpr int NITEM = G::HD * HH * NSEG;
   static_assert(SRC != 3 || NITEM <= 512, "one staging item per thread");
   constexpr int NREG = SRC == 3 ? 8 : MAXK;          // uint4 registers per set
-  constexpr int PD = MB * NB <= 4 ? 2 : 1;           // fragment read-ahead (steps)
+  constexpr int PD = MB * NB <= 4 ? 3 : 1;           // fragment read-ahead (steps)
   constexpr int HOOK = 1;                            // step after which the next stage is staged
 
   const int tid = threadIdx.x;
@@ -242,6 +242,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   const int wslots = WF ? a.nchunks * WFRAG : 2 * WFRAG;
   float* btab = reinterpret_cast<float*>(wts + wslots);  // bias per packed column (16-byte aligned)
   const int nbcol = a.nbt_pad * 32;
+  uint4* const trash = reinterpret_cast<uint4*>(btab + nbcol) + tid;  // one 16-byte slot per thread
 
   // Job assignment.  Workgroups are dealt to the 8 XCDs round-robin; each XCD
   // owns a contiguous eighth of the jobs, and inside it its workgroups take
@@ -372,24 +373,24 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   auto commit_act = [&](int slot, int buf) __attribute__((always_inline)) {
     if constexpr (SRC == 3) {
       // 8 channels x 8 positions -> 8 slots of 8 channels (position p of
-      // channel e is half p of pfa[e]).
+      // channel e is half p of pfa[e]).  A position outside the tile row goes
+      // to this thread's trash slot instead of behind a branch.
       if (item >= 0) {
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          if (seg_mask & (1 << p)) {
-            const uint32_t sel = (p & 1) ? 0x07060302u : 0x05040100u;
-            const int m = p >> 1;
-            u32x4_t v;
+          const uint32_t sel = (p & 1) ? 0x07060302u : 0x05040100u;
+          const int m = p >> 1;
+          u32x4_t v;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint4& lo = pfa[slot][2 * q];
-              const uint4& hi = pfa[slot][2 * q + 1];
-              const uint32_t l = m == 0 ? lo.x : (m == 1 ? lo.y : (m == 2 ? lo.z : lo.w));
-              const uint32_t h = m == 0 ? hi.x : (m == 1 ? hi.y : (m == 2 ? hi.z : hi.w));
-              v[q] = __builtin_amdgcn_perm(h, l, sel);
-            }
-            *reinterpret_cast<u32x4_t*>(act + buf * HPAD + seg_hw + p) = v;
+          for (int q = 0; q < 4; ++q) {
+            const uint4& lo = pfa[slot][2 * q];
+            const uint4& hi = pfa[slot][2 * q + 1];
+            const uint32_t l = m == 0 ? lo.x : (m == 1 ? lo.y : (m == 2 ? lo.z : lo.w));
+            const uint32_t h = m == 0 ? hi.x : (m == 1 ? hi.y : (m == 2 ? hi.z : hi.w));
+            v[q] = __builtin_amdgcn_perm(h, l, sel);
           }
+          uint4* const dst = (seg_mask & (1 << p)) ? act + buf * HPAD + seg_hw + p : trash;
+          *reinterpret_cast<u32x4_t*>(dst) = v;
         }
       }
       return;
@@ -511,7 +512,8 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
       }
     };
     read_step(std::integral_constant<int, 0>{}, 0);
-    if constexpr (PD == 2) read_step(std::integral_constant<int, 1>{}, 1);
+    if constexpr (PD >= 2) read_step(std::integral_constant<int, 1>{}, 1);
+    if constexpr (PD >= 3) read_step(std::integral_constant<int, 2>{}, 2);
     static_for(std::make_integer_sequence<int, NSTEP>{}, step);
     if (cc.chunk == (cc.split + 1) * a.cps - 1) {
       if (a.nsplit > 1) store_partial(cc);
