@@ -510,14 +510,24 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   p.copy_bytes = 0;
   // A w-contiguous k=3 source (NCDHW) is staged by 16-byte loads of 8
   // positions per channel and a register transpose (tap kernel staging mode 3).
+  // The channel planes must be outermost in a sample (a plane's positions, up
+  // to the end of its last 8-position load, below the channel stride): the
+  // kernel's buffer range then ends at channel cs.
   const bool k3_wvec = p.mode == MODE_K3 && a.ss[4] == 1 && a.ss[1] != 1 && sw % 8 == 0 && a.ss[0] % 8 == 0 &&
-                       a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 && a.pw >= -6 && a.pw <= 8;
+                       a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 && a.pw >= -6 && a.pw <= 8 &&
+                       a.ss[2] > 0 && a.ss[3] > 0 &&
+                       a.ss[1] >= (int64_t)(sdd - 1) * a.ss[2] + (int64_t)(sh - 1) * a.ss[3] + sw &&
+                       2 * (int64_t)cs * a.ss[1] < (1ll << 30);
   if (!k3_wvec && p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
     p.copy_bytes = align256(tensor_bytes(d->n, cs, sdd, sh, sw));
     channels_last_strides(a.ss, cs, sdd, sh, sw);
   }
   a.src_bytes = sample_bytes(a.ss, cs, sdd, sh, sw);
   a.dst_bytes = sample_bytes(a.sd, a.ncols, a.Rd, a.Rh, a.Rw);
+  // NCDHW k=3 staging: the buffer range ends exactly at channel cs, so loads
+  // of the channels past it need no gating.
+  a.chan_outer = k3_wvec ? 1 : 0;
+  if (k3_wvec) a.src_bytes = (uint32_t)(2 * (int64_t)cs * a.ss[1]);
   // Channel-contiguous sources are staged by direct-to-LDS 16-byte loads;
   // others by 8 scalar loads per slot through registers.
   p.cl = (a.ss[1] == 1 && cs % 8 == 0 && a.ss[0] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 &&

@@ -55,6 +55,8 @@ struct RowArgs {
   int32_t t2kw;            // T2FWD: 1 = columns ((kd, kh), co, kw) with kw fastest (w-contiguous output),
                            //        0 = columns (tap, co)
   int32_t phase;           // 0: main pass; 1: split-K epilogue pass, one workgroup per tile
+  int32_t chan_outer;      // 1: src_bytes ends at channel Cs (channel planes outermost in a sample),
+                           //    so loads of channels past Cs fall out of range by themselves
 };
 
 // Weight-gradient box geometry, fixed per mode: TD x TH lines of 16

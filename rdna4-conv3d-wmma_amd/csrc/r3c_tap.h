@@ -199,7 +199,8 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
 }
 
 // SRC: 1 = channel-contiguous source (16-byte slot loads), 0 = any strides
-// (eight 2-byte loads per slot), 3 = w-contiguous source (NCDHW, W % 8 == 0):
+// (eight 2-byte loads per slot), 3 = w-contiguous source with channel planes
+// outermost in a sample (NCDHW, W % 8 == 0, RowArgs::chan_outer):
 // a thread loads 8 positions of each of the chunk's 8 channels (eight 16-byte
 // loads of one tile row segment) and transposes them in registers into 8 slots.
 // WF: every chunk's weights resident in LDS (single column tile), else two
@@ -242,7 +243,8 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   const int wslots = WF ? a.nchunks * WFRAG : 2 * WFRAG;
   float* btab = reinterpret_cast<float*>(wts + wslots);  // bias per packed column (16-byte aligned)
   const int nbcol = a.nbt_pad * 32;
-  uint4* const trash = reinterpret_cast<uint4*>(btab + nbcol) + tid;  // one 16-byte slot per thread
+  // One 16-byte trash slot per thread past the bias table, as a slot index of `act`.
+  const uint32_t tslot = (uint32_t)((reinterpret_cast<uint4*>(btab + nbcol) + tid) - act);
 
   // Job assignment.  Workgroups are dealt to the 8 XCDs round-robin; each XCD
   // owns a contiguous eighth of the jobs, and inside it its workgroups take
@@ -339,18 +341,24 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
   auto issue_act = [&](const TapCursor& cur, int slot, bool live) __attribute__((always_inline)) {
     job_offsets(cur);
     const int c0 = live ? cur.chunk * 8 : 0;
-    const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), a.src_bytes);
     const uint32_t coff = live ? 2u * c0 * ss1 : 0u;  // uniform
     // Disabled loads get bit 31 set in their offset: past any num_records
     // (every valid offset is below 1 GiB), by arithmetic rather than a select,
     // which the compiler would turn into branches around duplicated loads.
     auto gate = [&](uint32_t off, bool on) { return (int)(off | ((uint32_t)!on << 31)); };
     if constexpr (SRC == 3) {
+      // The host takes this mode only with channel planes outermost in a
+      // sample and the buffer range ending at channel Cs, so loads of channels
+      // past Cs fall out of range by themselves; a stage past the end gets an
+      // empty range.  No per-load gating.
+      const __amdgpu_buffer_rsrc_t src =
+          make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), live ? a.src_bytes : 0u);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         pfa[slot][e] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, gate(soff[0] + coff + 2u * e * ss1, live && c0 + e < a.Cs), 0, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)(soff[0] + coff + 2u * e * ss1), 0, 0));
     } else {
+      const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), a.src_bytes);
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {
       if (SRC == 1) {
@@ -389,8 +397,11 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
             const uint32_t h = m == 0 ? hi.x : (m == 1 ? hi.y : (m == 2 ? hi.z : hi.w));
             v[q] = __builtin_amdgcn_perm(h, l, sel);
           }
-          uint4* const dst = (seg_mask & (1 << p)) ? act + buf * HPAD + seg_hw + p : trash;
-          *reinterpret_cast<u32x4_t*>(dst) = v;
+          // Slot index by masking (no select of pointers, which the compiler
+          // turns into a branch per position).
+          const uint32_t keep = 0u - (uint32_t)((seg_mask >> p) & 1);
+          const uint32_t slot_i = tslot ^ (((uint32_t)(buf * HPAD + seg_hw + p) ^ tslot) & keep);
+          *reinterpret_cast<u32x4_t*>(act + slot_i) = v;
         }
       }
       return;
