@@ -517,7 +517,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
                        a.ss[1] % 8 == 0 && a.ss[2] % 8 == 0 && a.ss[3] % 8 == 0 && a.pw >= -6 && a.pw <= 8 &&
                        a.ss[2] > 0 && a.ss[3] > 0 &&
                        a.ss[1] >= (int64_t)(sdd - 1) * a.ss[2] + (int64_t)(sh - 1) * a.ss[3] + sw &&
-                       2 * (int64_t)cs * a.ss[1] < (1ll << 30);
+                       2 * (int64_t)(cs + 8) * a.ss[1] < (1ll << 30);  // no 32-bit wrap past the last chunk
   if (!k3_wvec && p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
     p.copy_bytes = align256(tensor_bytes(d->n, cs, sdd, sh, sw));
     channels_last_strides(a.ss, cs, sdd, sh, sw);
@@ -944,8 +944,12 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   // It loads 1.8x the bytes of NDHWC staging plus the transposes, which costs
   // more than the copy saves above 64 G channels (measured: 24 and 48 channels
   // gain 52 and 22 us per trunk pass, 96 loses 15, 192 breaks even).
+  // The channel planes must be outermost in a sample: G's buffer range then
+  // ends at channel Gc and the kernel gates no channel.
   if (p.fl == 1 && p.mode == MODE_K3 && a.Gc <= 64 && a.gs[4] == 1 && a.Gw % 8 == 0 && a.gs[0] % 8 == 0 &&
-      a.gs[1] % 8 == 0 && a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0 && a.pw >= 0 && a.pw <= 6)
+      a.gs[1] % 8 == 0 && a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0 && a.pw >= 0 && a.pw <= 6 && a.gs[2] > 0 &&
+      a.gs[3] > 0 && a.gs[1] >= (int64_t)(a.Gd - 1) * a.gs[2] + (int64_t)(a.Gh - 1) * a.gs[3] + a.Gw &&
+      2 * (int64_t)(a.Gc + 8) * a.gs[1] < (1ll << 30))  // no 32-bit wrap past the last channel group
     p.fl = 3;
   if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
     p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
@@ -956,7 +960,7 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
     channels_last_strides(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   }
   a.f_bytes = sample_bytes(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
-  a.g_bytes = sample_bytes(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
+  a.g_bytes = p.fl == 3 ? (uint32_t)(2 * (int64_t)a.Gc * a.gs[1]) : sample_bytes(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   // G channel range per tile: a multiple of 8 (16-byte staging) and of 4 (quads).
   if (a.Gc <= 32) a.GCW = (a.Gc + 7) / 8 * 8;
   else if (a.Gc % 32 == 0) a.GCW = 32;

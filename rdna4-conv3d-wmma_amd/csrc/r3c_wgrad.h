@@ -340,14 +340,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         if (k > 0 && wvu != XW) break;  // wave-uniform: only wave XW holds second items
         const int c = gwcode[k];
         const int gd = s0d + (c & 255), gh = s0h + ((c >> 8) & 255), gw = r0w - 8 + 8 * ((c >> 16) & 255);
-        const int ch0 = gc0 + 8 * ((c >> 24) & 255);
         const bool ok = live & (c >= 0) & ((unsigned)gd < (unsigned)a.Gd) & ((unsigned)gh < (unsigned)a.Gh) &
                         ((unsigned)gw < (unsigned)a.Gw);
         const int off = gb3 + gwrel[k];
+        // G's buffer range ends at channel Gc (the host takes FL 3 only with
+        // channel planes outermost), so channels past it need no gating; the
+        // per-lane position gate is applied to each full offset (an edge
+        // item's offset may be negative, and bit 31 must survive the channel
+        // offset).
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           pgw[k][e] = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, gate(off + 2 * e * gs1, ok & (ch0 + e < a.Gc)), 0, 0));
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gsrc, gate(off + 2 * e * gs1, ok), 0, 0));
       }
       return;
     }
@@ -379,7 +383,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       // eight channels of position p (v_perm picks the 16-bit halves).  A
       // position outside the tile row is written to this thread's trash slot
       // (past both buffers) instead of being branched around.
-      uint16_t* const trash = tiles + 2 * TILE + tid * 8;
+      // Offsets in halves from `tiles`, chosen by masking (a select of
+      // pointers becomes a branch per position).
+      const uint32_t toff = (uint32_t)(2 * TILE + tid * 8);
+      const uint32_t gbase = (uint32_t)(gtl - tiles);
 #pragma unroll
       for (int k = 0; k < NGW; ++k) {
         if (k > 0 && wvu != XW) break;
@@ -389,8 +396,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
           u32x4_t v;
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = __builtin_amdgcn_perm(pgw[k][2 * q + 1][p >> 1], pgw[k][2 * q][p >> 1], sel);
-          uint16_t* const dst = (gwmask[k] & (1 << p)) ? gtl + gwslot[k] + p * 32 : trash;
-          *reinterpret_cast<u32x4_t*>(dst) = v;
+          const uint32_t keep = 0u - (uint32_t)((gwmask[k] >> p) & 1);
+          const uint32_t o = toff ^ (((gbase + (uint32_t)(gwslot[k] + p * 32)) ^ toff) & keep);
+          *reinterpret_cast<u32x4_t*>(tiles + o) = v;
         }
       }
       return;
