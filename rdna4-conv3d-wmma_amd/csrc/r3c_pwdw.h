@@ -109,8 +109,8 @@ __global__ __launch_bounds__(512) void pwdw_kernel(const PwdwArgs a) {
     const int p0 = live ? kb * KB : 0;  // N * S < 2^31 (host)
     const int n = p0 / a.S;
     const int s0 = p0 - n * a.S;
-    const __amdgpu_buffer_rsrc_t fr = make_rsrc(a.fsrc + (int64_t)n * a.fs0, a.f_bytes);
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gsrc + (int64_t)n * a.gs0, a.g_bytes);
+    const __amdgpu_buffer_rsrc_t fr = make_rsrc_u(a.fsrc + (int64_t)n * a.fs0, a.f_bytes);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc_u(a.gsrc + (int64_t)n * a.gs0, a.g_bytes);
     uint32_t gu;  // uniform G offset (bytes)
     if (MODE == MODE_T2DW) {
       const int d = s0 / a.HW, rem = s0 - d * a.HW;

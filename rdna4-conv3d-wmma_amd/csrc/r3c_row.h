@@ -99,6 +99,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// The same for a base and range that are equal in every lane but computed on
+// the vector unit (divisions, 64-bit products): readfirstlane moves them to
+// scalar registers.  A resource left in vector registers makes the compiler
+// wrap every buffer load in a readfirstlane / compare / exec-mask loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_u(const void* base, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
+
 // Half k of element q of a uint4 (q in 0..7), without taking its address.
 __device__ __forceinline__ uint16_t u4_elem(const uint4& v, int q) {
   const uint32_t w = q < 2 ? v.x : (q < 4 ? v.y : (q < 6 ? v.z : v.w));

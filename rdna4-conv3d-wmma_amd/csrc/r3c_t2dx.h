@@ -77,7 +77,7 @@ __global__ __launch_bounds__(512) void t2dx_kernel(const T2dxArgs a) {
   // `set`; a stage past the end is loaded with every offset out of range
   // (zeros, no memory access), which keeps the compiler's load counting exact.
   auto issue = [&](const Pos& P, int kc, int set, bool live) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t src = make_rsrc(a.dy + (live ? (int64_t)P.n * a.ys0 : 0), a.dy_bytes);
+    const __amdgpu_buffer_rsrc_t src = make_rsrc_u(a.dy + (live ? (int64_t)P.n * a.ys0 : 0), a.dy_bytes);
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
       const int co = 2 * (kc * KC + j) + g;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(512) void t2dx_kernel(const T2dxArgs a) {
     for (int e = 0; e < 16; ++e) acc[rb][e] = 0.f;
 
   auto epilogue = [&](const Pos& P) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.dx + (int64_t)P.n * a.xs0, a.dx_bytes);
+    const __amdgpu_buffer_rsrc_t dst = make_rsrc_u(a.dx + (int64_t)P.n * a.xs0, a.dx_bytes);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll

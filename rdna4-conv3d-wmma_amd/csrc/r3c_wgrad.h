@@ -267,15 +267,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   struct BoxCur {
     int bw, bh, bd, n, box;
   };
+  // The divisions run on the vector unit; readfirstlane puts the (uniform)
+  // results back in scalar registers, so buffer resources built from them are
+  // scalar too.  A resource in vector registers makes the compiler wrap every
+  // buffer load in a readfirstlane / compare / exec-mask loop.
   auto box_at = [&](int box) {
     BoxCur c;
+    box = __builtin_amdgcn_readfirstlane(box);
     c.box = box;
-    c.bw = box % a.nbw;
-    box /= a.nbw;
-    c.bh = box % a.nbh;
-    box /= a.nbh;
-    c.bd = box % a.nbd;
-    c.n = box / a.nbd;
+    c.bw = __builtin_amdgcn_readfirstlane(box % a.nbw);
+    box = __builtin_amdgcn_readfirstlane(box / a.nbw);
+    c.bh = __builtin_amdgcn_readfirstlane(box % a.nbh);
+    box = __builtin_amdgcn_readfirstlane(box / a.nbh);
+    c.bd = __builtin_amdgcn_readfirstlane(box % a.nbd);
+    c.n = __builtin_amdgcn_readfirstlane(box / a.nbd);
     return c;
   };
   auto box_advance = [&](BoxCur& c) {
@@ -316,8 +321,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       s0h = r0h - a.ph;
       s0w = r0w - a.pw;
     }
-    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc(a.fsrc + (live ? (int64_t)cur.n * a.fs[0] : 0), a.f_bytes);
-    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc(a.gsrc + (live ? (int64_t)cur.n * a.gs[0] : 0), a.g_bytes);
+    const __amdgpu_buffer_rsrc_t fsrc = make_rsrc_u(a.fsrc + (live ? (int64_t)cur.n * a.fs[0] : 0), a.f_bytes);
+    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc_u(a.gsrc + (live ? (int64_t)cur.n * a.gs[0] : 0), a.g_bytes);
     const int fbase = 2 * (r0d * fs2 + r0h * fs3 + r0w * fs4);
     const int gbase = 2 * (s0d * gs2 + s0h * gs3 + s0w * gs4);
     const bool f_in = r0d + Geo::TD <= a.Rd && r0h + TH <= a.Rh && r0w + 16 <= a.Rw;
