@@ -152,6 +152,11 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
   const bool ch_contig = !pos_contig && sd[1] == 1;
   const int sd1 = (int)sd[1], sd2 = (int)sd[2], sd3 = (int)sd[3], sd4 = (int)sd[4];
   auto gate = [](uint32_t off, bool on) { return (int)(off | ((uint32_t)!on << 31)); };
+  // Uniform: the whole box lies inside the volume.  A group of 8 columns of
+  // such a box that lies inside the real columns is stored without gates
+  // (the common case); only edge boxes and the last column group pay for the
+  // per-store tests.
+  const bool box_in = r0d + TD <= a.Rd && r0h + TH * HR <= a.Rh && r0w + LW <= a.Rw;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int r = wv * MB + mb;
@@ -172,19 +177,27 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
         const float4 bv = bt[2 * q];
         const float v0 = acc[mb][nb][4 * q + 0] + bv.x, v1 = acc[mb][nb][4 * q + 1] + bv.y;
         const float v2 = acc[mb][nb][4 * q + 2] + bv.z, v3 = acc[mb][nb][4 * q + 3] + bv.w;
+        const bool clean = box_in && colbase + 8 * q + 8 <= a.ncols;  // uniform
         if (pos_contig || !ch_contig) {
           const float vv[4] = {v0, v1, v2, v3};
+          if (clean) {
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const uint32_t off = poff + 2u * (uint32_t)((c0 + rr) * sd1);
-            __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off, pos_ok && c0 + rr < a.ncols), 0, 0);
+            for (int rr = 0; rr < 4; ++rr)
+              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst,
+                                                    (int)(poff + 2u * (uint32_t)((c0 + rr) * sd1)), 0, 0);
+          } else {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const uint32_t off = poff + 2u * (uint32_t)((c0 + rr) * sd1);
+              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off, pos_ok && c0 + rr < a.ncols), 0, 0);
+            }
           }
         } else {
           typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
           const uint32_t off = poff + 2u * (uint32_t)c0;
           if (c0 + 4 <= a.ncols) {
             const u32x2_t v = {pack2(from_f32<T>(v0), from_f32<T>(v1)), pack2(from_f32<T>(v2), from_f32<T>(v3))};
-            __builtin_amdgcn_raw_buffer_store_b64(v, dst, gate(off, pos_ok), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(v, dst, clean ? (int)off : gate(off, pos_ok), 0, 0);
           } else {
             const float vv[4] = {v0, v1, v2, v3};
 #pragma unroll
