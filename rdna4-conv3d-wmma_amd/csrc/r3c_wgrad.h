@@ -283,19 +283,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     c.n = __builtin_amdgcn_readfirstlane(box / a.nbd);
     return c;
   };
+  // Next box of this split: box + s8, as a digit-wise add of s8's digits
+  // (w fastest) with carries -- each digit sum is below twice its radix, so
+  // one conditional subtraction normalises it; no divisions per box.
+  const BoxCur sdig = box_at(s8);
   auto box_advance = [&](BoxCur& c) {
-    if (s8 != 1) {
-      c = box_at(c.box + s8);
-      return;
-    }
-    ++c.box;
-    if (++c.bw < a.nbw) return;
-    c.bw = 0;
-    if (++c.bh < a.nbh) return;
-    c.bh = 0;
-    if (++c.bd < a.nbd) return;
-    c.bd = 0;
-    ++c.n;
+    c.box += s8;
+    int v = c.bw + sdig.bw;
+    int cy = v >= a.nbw;
+    c.bw = cy ? v - a.nbw : v;
+    v = c.bh + sdig.bh + cy;
+    cy = v >= a.nbh;
+    c.bh = cy ? v - a.nbh : v;
+    v = c.bd + sdig.bd + cy;
+    cy = v >= a.nbd;
+    c.bd = cy ? v - a.nbd : v;
+    c.n += sdig.n + cy;
   };
   // Loads of one box into the staging registers.  A box whose tile lies
   // inside the volume (the common case) takes the precomputed validity; one
