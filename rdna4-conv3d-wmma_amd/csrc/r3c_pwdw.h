@@ -45,7 +45,7 @@ __global__ __launch_bounds__(512) void pwdw_kernel(const PwdwArgs a) {
   constexpr int GL = MODE == MODE_T2DW ? 2 : 1;  // 16-byte G loads per MFMA fragment
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, known wave-uniform
   const int g = lane >> 5;
   const int li = lane & 31;
 

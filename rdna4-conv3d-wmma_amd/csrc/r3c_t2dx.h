@@ -37,7 +37,7 @@ __global__ __launch_bounds__(512) void t2dx_kernel(const T2dxArgs a) {
   extern __shared__ uint4 afr[];  // [RB][nks][64] A fragments of this row group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, known wave-uniform
   const int g = lane >> 5;
   const int li = lane & 31;
   const int nks = a.nks;

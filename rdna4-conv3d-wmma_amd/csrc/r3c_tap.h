@@ -248,7 +248,7 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, known wave-uniform
   const int g = lane >> 5;
   const int li = lane & 31;
   uint4* act = smem4;              // [2][HPAD]
