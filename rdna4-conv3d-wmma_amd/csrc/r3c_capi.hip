@@ -552,8 +552,10 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   p.ck = 8 * g8;
   const int nbt = cdiv(a.ncols, 32);
   static const int opts[] = {3, 2, 1};
-  p.nb = pick_blocks(nbt, opts, 3);
-  const int rows = p.mode == MODE_T2DX ? 4 : 8;  // 4 waves x MB row blocks
+  static const int opts_t2[] = {6, 3, 2, 1};  // ConvTranspose fwd: one row block per wave
+  p.nb = p.mode == MODE_T2FWD ? pick_blocks(nbt, opts_t2, 4) : pick_blocks(nbt, opts, 3);
+  const bool mb1 = p.mode == MODE_T2DX || p.mode == MODE_T2FWD;  // the kernel's RowGeom::MB == 1
+  const int rows = mb1 ? 4 : 8;  // 4 waves x MB row blocks
   if (p.mode == MODE_K3) pick_box(rows, a.Rd, a.Rh, 2, 2, 4, a.TD, a.TH);
   else pick_box(rows, a.Rd, a.Rh, 0, 1, rows, a.TD, a.TH);
   a.nbd = cdiv(a.Rd, a.TD);
@@ -618,7 +620,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
   }
   a.nsplit = split;
   a.cps = a.nchunks / split;
-  const int mb = p.mode == MODE_T2DX ? 1 : 2;
+  const int mb = mb1 ? 1 : 2;
   p.part_bytes = split > 1 ? align256(p.ntiles * split * 4 * mb * p.nb * 16 * 64 * 4) : 0;
 }
 

@@ -70,7 +70,10 @@ struct RowGeom {
   static constexpr int HW = MODE == MODE_K3 ? 34 : (MODE == MODE_T2DX ? 64 : 32);
   // Row blocks (32 positions) per wave, and the largest LDS tile any allowed box
   // needs (K3: 2x4 or 4x2 boxes plus halo; T2DX: boxes of 4 rows, 2x in dY).
-  static constexpr int MB = MODE == MODE_T2DX ? 1 : 2;
+  // ConvTranspose fwd has 8 Cout columns per source channel: one row block per
+  // wave leaves the registers for six column blocks, so a 24-channel output
+  // (192 columns) is one column tile and each source box is staged once.
+  static constexpr int MB = (MODE == MODE_T2DX || MODE == MODE_T2FWD) ? 1 : 2;
   static constexpr int MAXHPOS = MODE == MODE_K3 ? 4 * 6 * 34 : (MODE == MODE_T2DX ? 16 * 64 : 8 * 32);
   // A chunk is G8 8-channel groups: one group per tap when there are taps; four
   // (two MFMA steps) for the memory-bound single-tap modes, so each pipeline

@@ -76,6 +76,30 @@ bool launch_row_t2fwd_f16(int nb, int cl, int wf, const RowArgs& a, int cus, siz
     launch_row_inst<f16_tag, MODE_T2FWD, 3, 0, 0>(a, cus, lds, s);
     return true;
   }
+  if (wf == 1 && cl == 2 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 2, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 1 && cl == 1 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 1, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 1 && cl == 0 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 0, 1>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 2 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 2, 0>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 1 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 1, 0>(a, cus, lds, s);
+    return true;
+  }
+  if (wf == 0 && cl == 0 && nb == 6) {
+    launch_row_inst<f16_tag, MODE_T2FWD, 6, 0, 0>(a, cus, lds, s);
+    return true;
+  }
   return false;
 }
 
