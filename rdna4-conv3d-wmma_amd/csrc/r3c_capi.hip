@@ -993,6 +993,15 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   // each extra split costs partial traffic.
   const int64_t wg_target = (int64_t)kNumCUs * std::max<int64_t>(1, kMaxLds / lds);
   int64_t nsplit = cdiv(wg_target, tiles);
+  // Each split writes its fp32 partial sums and the reduce reads them back.
+  // Where those would outweigh the operands (many channels over few
+  // positions), half the splits is faster: fewer partial bytes, and each
+  // workgroup's prologue and partial write-out cover twice the boxes
+  // (measured: 96->96 dW pass 101 -> 90 us, 192->192 73 -> 62 us; a quarter
+  // is slower again, 133 and 79 us).
+  const int64_t op_bytes =
+      2 * (int64_t)d->n * ((int64_t)a.Fc * a.Rd * a.Rh * a.Rw + (int64_t)a.Gc * a.Gd * a.Gh * a.Gw);
+  if (nsplit * per_split > op_bytes) nsplit = std::max<int64_t>(1, nsplit / 2);
   nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, nbox));
   a.nsplit = (int32_t)nsplit;
