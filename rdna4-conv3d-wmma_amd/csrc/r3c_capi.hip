@@ -945,7 +945,8 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   // Its 8-aligned w segments [r0w - 8, r0w + 24) cover the halo row for pw <= 6.
   // It loads 1.8x the bytes of NDHWC staging plus the transposes, which costs
   // more than the copy saves above 64 G channels (measured: 24 and 48 channels
-  // gain 52 and 22 us per trunk pass, 96 loses 15, 192 breaks even).
+  // gain 52 and 22 us per trunk pass, 96 loses 15, 192 breaks even; with the
+  // halved splits below, 96 loses 3.5 us and 192 gains 2).
   // The channel planes must be outermost in a sample: G's buffer range then
   // ends at channel Gc and the kernel gates no channel.
   if (p.fl == 1 && p.mode == MODE_K3 && a.Gc <= 64 && a.gs[4] == 1 && a.Gw % 8 == 0 && a.gs[0] % 8 == 0 &&
