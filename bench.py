@@ -167,21 +167,81 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2):
     return UNet3D()
 
 
-def unet3d_train(conv, tr, base, x, labels, steps, warmup):
-    """AMP bf16 training of build_unet3d(conv, tr, base) on (x, labels):
-    cross-entropy, Adam(lr=1e-3).  Weights are seeded (seed 1) before the build,
-    so two calls with different layer classes start from identical weights.
+def _rounded_layers():
+    """Conv3d / ConvTranspose3d whose arithmetic is fp32 on the autocast-dtype
+    operands, with every result (y, dX, dW, db) rounded once to that dtype:
+    a correctly rounded half-precision convolution.  Used as the second correct
+    half-precision implementation in the loss-spread control (stock MIOpen is
+    the first): the two differ only in how each convolution sums and rounds."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    def amp_cast(*ts):
+        if not torch.is_autocast_enabled("cuda"):
+            return ts
+        dt = torch.get_autocast_dtype("cuda")
+        return tuple(None if t is None else t.to(dt) for t in ts)
+
+    class _Fn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, w, b, transpose, stride, padding):
+            ctx.save_for_backward(x, w)
+            ctx.cfg = (transpose, stride, padding, b is not None, None if b is None else b.dtype)
+            f = F.conv_transpose3d if transpose else F.conv3d
+            with torch.autocast("cuda", enabled=False):
+                y = f(x.float(), w.float(), None if b is None else b.float(), stride, padding)
+            return y.to(x.dtype)
+
+        @staticmethod
+        def backward(ctx, go):
+            x, w = ctx.saved_tensors
+            transpose, stride, padding, has_b, b_dtype = ctx.cfg
+            with torch.enable_grad(), torch.autocast("cuda", enabled=False):
+                xf = x.detach().float().requires_grad_(True)
+                wf = w.detach().float().requires_grad_(True)
+                f = F.conv_transpose3d if transpose else F.conv3d
+                y = f(xf, wf, None, stride, padding)
+                gx, gw = torch.autograd.grad(y, (xf, wf), go.float())
+            gb = go.float().sum((0, 2, 3, 4)).to(b_dtype) if has_b else None
+            return gx.to(x.dtype), gw.to(w.dtype), gb, None, None, None
+
+    class RoundedConv3d(nn.Conv3d):
+        def forward(self, x):
+            x, w, b = amp_cast(x, self.weight, self.bias)
+            return _Fn.apply(x, w, b, False, self.stride, self.padding)
+
+    class RoundedConvTranspose3d(nn.ConvTranspose3d):
+        def forward(self, x, output_size=None):
+            x, w, b = amp_cast(x, self.weight, self.bias)
+            return _Fn.apply(x, w, b, True, self.stride, self.padding)
+
+    return RoundedConv3d, RoundedConvTranspose3d
+
+
+def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False):
+    """AMP training of build_unet3d(conv, tr, base) on (x, labels):
+    cross-entropy, Adam(lr=1e-3), autocast in `amp_dtype` (bf16 by default,
+    BASELINE config 5; torch.float16 is the reference's protocol,
+    benches/unet_e2e.py:47, whose torch.autocast("cuda") defaults to fp16), no
+    gradient scaler (as in the reference).  channels_last runs model and input
+    in channels_last_3d.  Weights are seeded (seed 1) before the build, so two
+    calls with different layer classes start from identical weights.
     Returns (ms per timed step, losses of every step in order)."""
     import torch
     import torch.nn as nn
+    amp_dtype = amp_dtype or torch.bfloat16
     torch.manual_seed(1)
     net = build_unet3d(conv, tr, base).to(x.device)
+    if channels_last:
+        net = net.to(memory_format=torch.channels_last_3d)
+        x = x.contiguous(memory_format=torch.channels_last_3d)
     opt = torch.optim.Adam(net.parameters(), lr=1e-3)
     loss_fn = nn.CrossEntropyLoss()
 
     def step():
         opt.zero_grad(set_to_none=True)
-        with torch.autocast("cuda", dtype=torch.bfloat16):
+        with torch.autocast("cuda", dtype=amp_dtype):
             y = net(x)
             loss = loss_fn(y, labels)
         loss.backward()

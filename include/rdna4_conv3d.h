@@ -3,7 +3,7 @@
  *
  * The library (librdna4_conv3d_hip.so) implements the hot path of the
  * reference package's autograd Functions as hand-written HIP kernels on CDNA4
- * bf16/fp16 MFMA (v_mfma_f32_16x16x32_{bf16,f16}, fp32 accumulate):
+ * bf16/fp16 MFMA (v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulate):
  *
  *   Conv3d k=1 / k=3, stride 1, dilation 1, groups 1: forward, dX, dW (+ fused db)
  *   ConvTranspose3d k=2, stride 2, pad 0:            forward, dX, dW (+ fused db)

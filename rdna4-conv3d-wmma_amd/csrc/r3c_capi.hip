@@ -443,7 +443,9 @@ void plan_tap(const r3c_conv_desc* d, RowPlan& p) {
   p.part_bytes = split > 1 ? align256(p.ntiles * split * 8 * p.mb * p.nb * 16 * 64 * 4) : 0;
 }
 
-void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
+// allow_copy false: never copy the source to NDHWC (its 16-byte copy kernel
+// needs an aligned source).
+void plan_row(const r3c_conv_desc* d, int op, RowPlan& p, bool allow_copy = true) {
   RowArgs& a = p.a;
   memset(&a, 0, sizeof a);
   const int k = d->kernel;
@@ -518,7 +520,7 @@ void plan_row(const r3c_conv_desc* d, int op, RowPlan& p) {
                        a.ss[2] > 0 && a.ss[3] > 0 &&
                        a.ss[1] >= (int64_t)(sdd - 1) * a.ss[2] + (int64_t)(sh - 1) * a.ss[3] + sw &&
                        2 * (int64_t)(cs + 8) * a.ss[1] < (1ll << 30);  // no 32-bit wrap past the last chunk
-  if (!k3_wvec && p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
+  if (allow_copy && !k3_wvec && p.mode == MODE_K3 && cs <= 32 && ncdhw_copyable(a.ss, cs, sdd, sh, sw)) {
     p.copy_bytes = align256(tensor_bytes(d->n, cs, sdd, sh, sw));
     channels_last_strides(a.ss, cs, sdd, sh, sw);
   }
@@ -686,8 +688,6 @@ int run_t2dx(const r3c_conv_desc* d, const T2dxPlan& p, const void* dy, const vo
   if (ws_bytes < p.wpk_bytes)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)p.wpk_bytes);
   if (!dy || !w || !dx || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
-  if ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dx)) & 3)
-    return fail(R3C_UNSUPPORTED, "ConvTranspose dX needs 4-byte aligned tensors");
   int rc = check_device();
   if (rc) return rc;
   T2dxPackArgs pk = p.pk;
@@ -711,19 +711,35 @@ int run_t2dx(const r3c_conv_desc* d, const T2dxPlan& p, const void* dy, const vo
   return check_launch("ConvTranspose dX kernel");
 }
 
+// Why a row plan cannot run (nullptr: it can).  The workspace query applies
+// the same checks, so a descriptor it accepts never fails on these grounds.
+const char* row_plan_reject(const RowPlan& p) {
+  if ((int64_t)p.lds > kMaxLds) return "the tile needs more LDS than a compute unit has";
+  if (p.a.src_bytes == 0) return "one input sample exceeds 1 GiB (32-bit buffer offsets)";
+  if (p.tap && p.a.dst_bytes == 0) return "one output sample exceeds 1 GiB (32-bit buffer offsets)";
+  if (p.ntiles * p.a.nsplit >= (1ll << 31)) return "grid too large";
+  return nullptr;
+}
+
+int64_t row_plan_ws(const RowPlan& p) { return align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes; }
+
+// The register-direct ConvTranspose dX loads 4-byte pairs; other alignments
+// take the row kernel (mode T2DX), which stages any alignment.
+bool t2dx_aligned(const void* dy, const void* dx) {
+  return ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dx)) & 3) == 0;
+}
+
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
             int64_t ws_bytes, void* stream) {
-  if (op == OP_T2_DX) {
+  if (op == OP_T2_DX && t2dx_aligned(src, dst)) {
     T2dxPlan tp;
     if (plan_t2dx(d, tp)) return run_t2dx(d, tp, src, w, dst, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
   }
   RowPlan p;
   plan_row(d, op, p);
-  if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
-  if (p.a.src_bytes == 0) return fail(R3C_UNSUPPORTED, "one input sample exceeds 1 GiB (32-bit buffer offsets)");
-  if (p.tap && p.a.dst_bytes == 0)
-    return fail(R3C_UNSUPPORTED, "one output sample exceeds 1 GiB (32-bit buffer offsets)");
-  const int64_t need = align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;
+  if (p.copy_bytes && (reinterpret_cast<uintptr_t>(src) & 15)) plan_row(d, op, p, false);  // same or less workspace
+  if (const char* why = row_plan_reject(p)) return fail(R3C_UNSUPPORTED, "%s", why);
+  const int64_t need = row_plan_ws(p);
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!src || !w || !dst || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
@@ -763,9 +779,7 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
     a.off32 = span < (1ll << 31) ? 1 : 0;
   }
   a.phase = 0;
-  const int64_t jobs = p.ntiles * a.nsplit;
-  if (jobs >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "grid too large");
-  a.njobs = (int32_t)jobs;
+  a.njobs = (int32_t)(p.ntiles * a.nsplit);  // below 2^31 (row_plan_reject)
   // The launcher sizes the grid to the resident capacity (CUs x workgroups
   // per CU from the occupancy query); workgroups take contiguous job ranges.
   TimedLaunch tl(KIND_ROW, s);
@@ -886,7 +900,9 @@ bool plan_pwdw(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   return true;
 }
 
-void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
+// allow_pw false: no register-direct plan (it needs 16-byte aligned sources);
+// allow_copy false: no NDHWC copy of an operand (likewise).
+void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw = true, bool allow_copy = true) {
   WgArgs& a = p.a;
   memset(&a, 0, sizeof a);
   if (transpose) {
@@ -908,13 +924,13 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
     memcpy(a.gs, d->x_strides, sizeof a.gs);
   }
   p.pw = 0;
-  if (plan_pwdw(d, transpose, p)) return;
+  if (allow_pw && plan_pwdw(d, transpose, p)) return;
   // NCDHW operands of the k=3 pass are copied to NDHWC first: the tiles are
   // [position][channel], which strided staging fills slowly, and the pass does
   // enough arithmetic per byte to pay for the copy.  The memory-bound k=1 and
   // ConvTranspose passes stage strided operands directly.
   p.fcopy_bytes = p.gcopy_bytes = 0;
-  const bool copy_ok = p.mode == MODE_K3;
+  const bool copy_ok = p.mode == MODE_K3 && allow_copy;
   // F needs no tap halo: a w-contiguous F (NCDHW) is staged channel-major
   // straight from the source (fl 1), with no copy.
   p.fl = (a.fs[4] == 1 && a.Rw % 8 == 0 && a.fs[0] % 8 == 0 && a.fs[1] % 8 == 0 && a.fs[2] % 8 == 0 &&
@@ -1022,8 +1038,6 @@ int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void
   PwdwArgs a = p.pa;
   a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
-  if ((reinterpret_cast<uintptr_t>(a.fsrc) | reinterpret_cast<uintptr_t>(a.gsrc)) & 15)
-    return fail(R3C_UNSUPPORTED, "single-tap weight gradient needs 16-byte aligned tensors");
   a.part = static_cast<float*>(ws);
   a.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
   a.db_mode = db ? (transpose ? 2 : 1) : 0;
@@ -1059,14 +1073,28 @@ int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void
   return check_launch("weight-gradient reduce");
 }
 
+// Why a weight-gradient plan cannot run (nullptr: it can); shared with the
+// workspace query.
+const char* wgrad_plan_reject(const WgPlan& p) {
+  if ((int64_t)p.lds > kMaxLds) return "the tile needs more LDS than a compute unit has";
+  if (!p.pw && (p.a.f_bytes == 0 || p.a.g_bytes == 0))  // the register-direct plan checks its own
+    return "one sample exceeds 1 GiB (32-bit buffer offsets)";
+  return nullptr;
+}
+
+int64_t wgrad_plan_ws(const WgPlan& p) {
+  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
+}
+
 int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void* dy, void* dw, int dw_dtype, void* db,
               int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
+  // The register-direct single-tap kernel loads 16-byte vectors; other
+  // alignments take the LDS-staged kernel, which stages any alignment.
+  const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0;
   WgPlan p;
-  plan_wgrad(d, transpose, p);
-  if ((int64_t)p.lds > kMaxLds) return fail(R3C_UNSUPPORTED, "tile needs %zu bytes of LDS", p.lds);
-  if (!p.pw && (p.a.f_bytes == 0 || p.a.g_bytes == 0))  // the register-direct plan checks its own
-    return fail(R3C_UNSUPPORTED, "one sample exceeds 1 GiB (32-bit buffer offsets)");
-  const int64_t need = p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
+  plan_wgrad(d, transpose, p, al16, al16);  // unaligned: no copies either (same or less workspace)
+  if (const char* why = wgrad_plan_reject(p)) return fail(R3C_UNSUPPORTED, "%s", why);
+  const int64_t need = wgrad_plan_ws(p);
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
@@ -1141,22 +1169,32 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   return check_launch("weight-gradient reduce");
 }
 
+// Workspace queries: -1 when the descriptor is invalid or no plan can run it
+// (the caller then falls back).  The size covers every plan the launch may
+// take for this descriptor, whatever the pointers' alignment.
 int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
-  if (op == OP_T2_DX) {
-    T2dxPlan tp;
-    if (plan_t2dx(d, tp)) return align256(tp.wpk_bytes);
-  }
   RowPlan p;
   plan_row(d, op, p);
-  return align256(p.wpk_bytes) + p.copy_bytes + p.part_bytes;
+  if (row_plan_reject(p)) return -1;
+  int64_t need = row_plan_ws(p);
+  if (op == OP_T2_DX) {
+    T2dxPlan tp;
+    if (plan_t2dx(d, tp)) need = std::max<int64_t>(need, align256(tp.wpk_bytes));
+  }
+  return need;
 }
 
 int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   WgPlan p;
-  plan_wgrad(d, transpose, p);
-  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
+  plan_wgrad(d, transpose, p, false);
+  if (wgrad_plan_reject(p)) return -1;
+  int64_t need = wgrad_plan_ws(p);
+  WgPlan q;
+  plan_wgrad(d, transpose, q, true);
+  if (q.pw) need = std::max<int64_t>(need, wgrad_plan_ws(q));
+  return need;
 }
 
 std::mutex g_dev_mu;

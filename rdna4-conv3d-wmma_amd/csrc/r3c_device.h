@@ -1,10 +1,11 @@
 // r3c_device.h -- device-side building blocks shared by the gfx950 kernels.
 //
-// Operand layouts of v_mfma_f32_16x16x32_{bf16,f16} (wave64), as used by every
-// kernel here (lane l, g = l / 16, j = l % 16):
-//   A (16 x 32): lane holds A[j][8g .. 8g+7]      (8 halves = 4 VGPRs)
-//   B (32 x 16): lane holds B[8g .. 8g+7][j]
-//   C (16 x 16): lane holds C[4g .. 4g+3][j]      (4 fp32)
+// Every matrix product here is v_mfma_f32_32x32x16_{bf16,f16} (wave64, fp32
+// accumulate).  Operand layouts (measured on gfx950; lane l, g = l / 32,
+// i = l % 32):
+//   A (32 x 16): lane holds A[i][8g .. 8g+7]      (8 halves = 4 VGPRs)
+//   B (16 x 32): lane holds B[8g .. 8g+7][i]
+//   C (32 x 32): acc[4q + r] = C[8q + 4g + r][i]  (16 fp32)
 // Any permutation of k applied to both A and B gives the same product, so the
 // only contract is the row/column placement above.
 //
@@ -12,7 +13,7 @@
 //   out[4a + b][i] = lds16[addr[a + 4i] + b]   (a, b, i in 0..3)
 // i.e. four source lanes each read 4 consecutive halves and the result is
 // handed out transposed.  Two such reads produce one MFMA operand whose k runs
-// over 8 tile rows (positions) while j runs over 16 contiguous channels.
+// over 8 tile rows (positions) while the lanes run over contiguous channels.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -42,17 +43,16 @@ struct f16_tag {
 };
 
 template <typename T>
-__device__ __forceinline__ f32x4_t mfma(const uint4& a, const uint4& b, const f32x4_t& c);
-
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const f32x16_t& c);
 template <>
-__device__ __forceinline__ f32x4_t mfma<bf16_tag>(const uint4& a, const uint4& b, const f32x4_t& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+__device__ __forceinline__ f32x16_t mfma32<bf16_tag>(const uint4& a, const uint4& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
 }
 template <>
-__device__ __forceinline__ f32x4_t mfma<f16_tag>(const uint4& a, const uint4& b, const f32x4_t& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+__device__ __forceinline__ f32x16_t mfma32<f16_tag>(const uint4& a, const uint4& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                0, 0, 0);
 }
 
 // Round-to-nearest-even conversions (IEEE definition; hardware cvt on gfx950).

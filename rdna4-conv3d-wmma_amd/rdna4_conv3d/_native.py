@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from functools import lru_cache
 from pathlib import Path
 from typing import Optional, Sequence, Tuple
 
@@ -217,8 +218,70 @@ def make_desc(x_shape, y_shape, kernel: int, padding, dtype: torch.dtype, x_stri
     return d
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+def _workspace(nbytes: int, device: torch.device, what: str) -> torch.Tensor:
+    """Workspace of the size the library asked for; a negative size means no
+    plan runs this descriptor (NativeUnsupported: the caller falls back)."""
+    if nbytes < 0:
+        raise NativeUnsupported(f"{what}: no native plan for this descriptor")
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _dense_strides(shape, channels_last: bool):
+    """Element strides of a dense NCDHW (or channels_last_3d) tensor of `shape`."""
+    n, c, d, h, w = (int(v) for v in shape)
+    if channels_last:
+        return (d * h * w * c, 1, h * w * c, w * c, c)
+    return (c * d * h * w, d * h * w, h * w, w, 1)
+
+
+def _passed_strides(t: torch.Tensor):
+    """Strides of the tensor the entry points pass on (see _dense)."""
+    if t.is_contiguous() or is_channels_last(t):
+        return tuple(int(v) for v in t.stride())
+    return _dense_strides(t.shape, False)
+
+
+def _out_channels_last(t: torch.Tensor) -> bool:
+    return is_channels_last(t) and not t.is_contiguous()
+
+
+@lru_cache(maxsize=4096)
+def _plans_ok(transpose: bool, x_shape, x_strides, y_shape, y_strides, kernel: int, padding, dtype_code: int) -> bool:
+    lib = load()
+    x_shape = tuple(x_shape)
+    d = ConvDesc()
+    d.dtype = dtype_code
+    d.n, d.cin, d.d, d.h, d.w = x_shape
+    _, d.cout, d.od, d.oh, d.ow = y_shape
+    d.kernel = kernel
+    d.pad_d, d.pad_h, d.pad_w = padding
+    for i in range(5):
+        d.x_strides[i] = x_strides[i]
+        d.y_strides[i] = y_strides[i]
+    names = ("convt_k2s2_fwd", "convt_k2s2_dx", "convt_k2s2_dw") if transpose else ("conv3d_fwd", "conv3d_dx",
+                                                                                       "conv3d_dw")
+    return all(getattr(lib, f"r3c_{nm}_workspace")(ctypes.byref(d)) >= 0 for nm in names)
+
+
+def conv_plans_ok(x: torch.Tensor, weight_shape, padding, dtype: torch.dtype) -> bool:
+    """True when the library has plans for this Conv3d's forward, dX and dW
+    (dY assumed in the output's layout, which follows x).  The workspace
+    queries return -1 for descriptors no plan runs, e.g. a sample of 1 GiB or
+    more (32-bit buffer offsets).  Cached per shape, strides and dtype."""
+    n, cin, d, h, w = (int(v) for v in x.shape)
+    k = int(weight_shape[2])
+    pd = tuple(int(p) for p in padding)
+    y_shape = (n, int(weight_shape[0]), d + 2 * pd[0] - k + 1, h + 2 * pd[1] - k + 1, w + 2 * pd[2] - k + 1)
+    return _plans_ok(False, tuple(x.shape), _passed_strides(x), y_shape,
+                     _dense_strides(y_shape, _out_channels_last(x)), k, pd, _DTYPE_CODE[dtype])
+
+
+def convt_plans_ok(x: torch.Tensor, weight_shape, dtype: torch.dtype) -> bool:
+    """conv_plans_ok for ConvTranspose3d k=2 s=2 (weight (Cin, Cout, 2, 2, 2))."""
+    n, cin, d, h, w = (int(v) for v in x.shape)
+    y_shape = (n, int(weight_shape[1]), 2 * d, 2 * h, 2 * w)
+    return _plans_ok(True, tuple(x.shape), _passed_strides(x), y_shape,
+                     _dense_strides(y_shape, _out_channels_last(x)), 2, (0, 0, 0), _DTYPE_CODE[dtype])
 
 
 # ---------------------------------------------------------------------------
@@ -235,7 +298,7 @@ def conv3d_fwd(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tenso
     od, oh, ow = (d + 2 * padding[0] - k + 1, h + 2 * padding[1] - k + 1, w + 2 * padding[2] - k + 1)
     y = out if out is not None else _empty_like_layout((n, cout, od, oh, ow), x, x.dtype)
     desc = make_desc(x.shape, y.shape, k, padding, x.dtype, x.stride(), y.stride())
-    ws = _workspace(lib.r3c_conv3d_fwd_workspace(ctypes.byref(desc)), x.device)
+    ws = _workspace(lib.r3c_conv3d_fwd_workspace(ctypes.byref(desc)), x.device, "r3c_conv3d_fwd")
     b = bias.contiguous() if bias is not None else None
     rc = lib.r3c_conv3d_fwd(ctypes.byref(desc), _ptr(x), _ptr(weight), _ptr(b), _ptr(y), _ptr(ws),
                             ws.numel(), _stream_handle(x.device))
@@ -251,7 +314,7 @@ def conv3d_dx(go: torch.Tensor, weight: torch.Tensor, x_shape, padding, like: to
     k = int(weight.shape[2])
     gx = _empty_like_layout(tuple(int(v) for v in x_shape), like, go.dtype)
     desc = make_desc(gx.shape, go.shape, k, padding, go.dtype, gx.stride(), go.stride())
-    ws = _workspace(lib.r3c_conv3d_dx_workspace(ctypes.byref(desc)), go.device)
+    ws = _workspace(lib.r3c_conv3d_dx_workspace(ctypes.byref(desc)), go.device, "r3c_conv3d_dx")
     rc = lib.r3c_conv3d_dx(ctypes.byref(desc), _ptr(go), _ptr(weight), _ptr(gx), _ptr(ws), ws.numel(),
                            _stream_handle(go.device))
     _check(lib, rc, "r3c_conv3d_dx")
@@ -270,7 +333,7 @@ def conv3d_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, padding, dw_dtype
     db = None
     if want_db:
         db = torch.empty((int(weight_shape[0]),), device=x.device, dtype=db_dtype or dw_dtype)
-    ws = _workspace(lib.r3c_conv3d_dw_workspace(ctypes.byref(desc)), x.device)
+    ws = _workspace(lib.r3c_conv3d_dw_workspace(ctypes.byref(desc)), x.device, "r3c_conv3d_dw")
     rc = lib.r3c_conv3d_dw(ctypes.byref(desc), _ptr(x), _ptr(go), _ptr(dw), _DTYPE_CODE[dw_dtype], _ptr(db),
                            _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws), ws.numel(),
                            _stream_handle(x.device))
@@ -289,7 +352,7 @@ def convt_fwd(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor
     cout = int(weight.shape[1])
     y = _empty_like_layout((n, cout, 2 * d, 2 * h, 2 * w), x, x.dtype)
     desc = make_desc(x.shape, y.shape, 2, (0, 0, 0), x.dtype, x.stride(), y.stride())
-    ws = _workspace(lib.r3c_convt_k2s2_fwd_workspace(ctypes.byref(desc)), x.device)
+    ws = _workspace(lib.r3c_convt_k2s2_fwd_workspace(ctypes.byref(desc)), x.device, "r3c_convt_k2s2_fwd")
     b = bias.contiguous() if bias is not None else None
     rc = lib.r3c_convt_k2s2_fwd(ctypes.byref(desc), _ptr(x), _ptr(weight), _ptr(b), _ptr(y), _ptr(ws),
                                 ws.numel(), _stream_handle(x.device))
@@ -303,7 +366,7 @@ def convt_dx(go: torch.Tensor, weight: torch.Tensor, x_shape, like: torch.Tensor
     weight = weight.contiguous()
     gx = _empty_like_layout(tuple(int(v) for v in x_shape), like, go.dtype)
     desc = make_desc(gx.shape, go.shape, 2, (0, 0, 0), go.dtype, gx.stride(), go.stride())
-    ws = _workspace(lib.r3c_convt_k2s2_dx_workspace(ctypes.byref(desc)), go.device)
+    ws = _workspace(lib.r3c_convt_k2s2_dx_workspace(ctypes.byref(desc)), go.device, "r3c_convt_k2s2_dx")
     rc = lib.r3c_convt_k2s2_dx(ctypes.byref(desc), _ptr(go), _ptr(weight), _ptr(gx), _ptr(ws), ws.numel(),
                                _stream_handle(go.device))
     _check(lib, rc, "r3c_convt_k2s2_dx")
@@ -320,7 +383,7 @@ def convt_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, dw_dtype: torch.dt
     db = None
     if want_db:
         db = torch.empty((int(weight_shape[1]),), device=x.device, dtype=db_dtype or dw_dtype)
-    ws = _workspace(lib.r3c_convt_k2s2_dw_workspace(ctypes.byref(desc)), x.device)
+    ws = _workspace(lib.r3c_convt_k2s2_dw_workspace(ctypes.byref(desc)), x.device, "r3c_convt_k2s2_dw")
     rc = lib.r3c_convt_k2s2_dw(ctypes.byref(desc), _ptr(x), _ptr(go), _ptr(dw), _DTYPE_CODE[dw_dtype], _ptr(db),
                                _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws), ws.numel(),
                                _stream_handle(x.device))

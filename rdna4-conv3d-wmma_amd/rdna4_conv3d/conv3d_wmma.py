@@ -32,6 +32,7 @@ Deliberate differences from the reference (each one a reference quirk):
 from __future__ import annotations
 
 import os
+import warnings
 from functools import lru_cache
 from typing import Optional, Tuple
 
@@ -158,7 +159,24 @@ def _conv_native_ok(x, weight, stride, padding, dilation) -> bool:
     sp = tuple(int(s) for s in x.shape[2:])
     if any(_out_size(L, ks[0], 1, p, 1) < 1 for L, p in zip(sp, pd)):
         return False
-    return _native_tensors_ok(x, weight)
+    if not _native_tensors_ok(x, weight):
+        return False
+    # The library must have plans for all three passes (e.g. not for a sample
+    # of 1 GiB or more); decided here, before the forward runs, so a native
+    # forward is never followed by an unsupported backward.
+    compute = x.dtype if x.dtype in _HALF else torch.float16
+    return _native.conv_plans_ok(x, weight.shape, pd, compute)
+
+
+_warned = set()
+
+
+def _fallback_warning(what: str, err: Exception) -> None:
+    """One warning per call site when the library declines a call it was
+    expected to run (R3C_UNSUPPORTED); the stock PyTorch routine runs instead."""
+    if what not in _warned:
+        _warned.add(what)
+        warnings.warn(f"rdna4_conv3d: {what} runs the stock PyTorch path: {err}", RuntimeWarning, stacklevel=3)
 
 
 def _ensure_native(device: torch.device) -> None:
@@ -196,8 +214,12 @@ class Conv3dWmmaFn(torch.autograd.Function):
         else:
             weight = weight.to(compute_dtype)
             bias = None if bias is None else bias.to(compute_dtype)
-        with torch.cuda.device(x.device):
-            y = _native.conv3d_fwd(x, weight, bias, _t3(padding))
+        try:
+            with torch.cuda.device(x.device):
+                y = _native.conv3d_fwd(x, weight, bias, _t3(padding))
+        except _native.NativeUnsupported as e:
+            _fallback_warning("Conv3d forward", e)
+            y = F.conv3d(x, weight, bias, stride, padding, dilation)
         if compute_dtype not in _HALF:
             y = y.to(compute_dtype)
         return y
@@ -223,11 +245,9 @@ class Conv3dWmmaFn(torch.autograd.Function):
         if not ctx.native:
             go = grad_out
             if need_x:
-                gx = torch.nn.grad.conv3d_input(x.shape, weight.to(go.dtype), go.contiguous(), stride, padding,
-                                                dilation, 1)
+                gx = _stock_dx(x, weight, go, stride, padding, dilation)
             if need_w:
-                dw = torch.nn.grad.conv3d_weight(x.to(go.dtype), weight.shape, go.contiguous(), stride, padding,
-                                                 dilation, 1).to(weight.dtype)
+                dw = _stock_dw(x, weight, go, stride, padding, dilation)
             if need_b:
                 db = go.sum(dim=(0, 2, 3, 4)).to(ctx.bias_dtype)
             return gx, dw, db, None, None, None
@@ -239,14 +259,22 @@ class Conv3dWmmaFn(torch.autograd.Function):
         with torch.cuda.device(x.device):
             if need_x:
                 w_c = weight if weight.dtype == half else weight.to(half)
-                gx = _native.conv3d_dx(go, w_c, x.shape, pad3, like=x)
+                try:
+                    gx = _native.conv3d_dx(go, w_c, x.shape, pad3, like=x)
+                except _native.NativeUnsupported as e:
+                    _fallback_warning("Conv3d dX", e)
+                    gx = _stock_dx(x, w_c, go, stride, padding, dilation)
                 if gx.dtype != x.dtype:
                     gx = gx.to(x.dtype)
             if need_w:
                 x_c = x if x.dtype == half else x.to(half)
                 dw_dtype = weight.dtype if weight.dtype == half else torch.float32
-                dw, db = _native.conv3d_dw(x_c, go, weight.shape, pad3, dw_dtype, want_db=need_b,
-                                           db_dtype=_db_dtype(ctx.bias_dtype, half))
+                try:
+                    dw, db = _native.conv3d_dw(x_c, go, weight.shape, pad3, dw_dtype, want_db=need_b,
+                                               db_dtype=_db_dtype(ctx.bias_dtype, half))
+                except _native.NativeUnsupported as e:
+                    _fallback_warning("Conv3d dW", e)
+                    dw, db = _stock_dw(x_c, weight, go, stride, padding, dilation), None
                 if dw.dtype != weight.dtype:
                     dw = dw.to(weight.dtype)
             if need_b and db is None:
@@ -254,6 +282,18 @@ class Conv3dWmmaFn(torch.autograd.Function):
             if need_b and db is not None and db.dtype != ctx.bias_dtype:
                 db = db.to(ctx.bias_dtype)
         return gx, dw, db, None, None, None
+
+
+def _stock_dx(x, weight, go, stride, padding, dilation):
+    """dX by PyTorch (MIOpen / oneDNN), in x's layout."""
+    gx = torch.nn.grad.conv3d_input(x.shape, weight.to(go.dtype), go.contiguous(), stride, padding, dilation, 1)
+    return _follow_layout(gx, x)
+
+
+def _stock_dw(x, weight, go, stride, padding, dilation):
+    """dW by PyTorch, in the weight's dtype."""
+    return torch.nn.grad.conv3d_weight(x.to(go.dtype), weight.shape, go.contiguous(), stride, padding, dilation,
+                                       1).to(weight.dtype)
 
 
 def _db_dtype(bias_dtype, half):
@@ -313,8 +353,13 @@ def wmma_fwd(x, weight, bias=None, stride=1, padding=0, dilation=1):
     if not _conv_native_ok(x, weight, st, pd, dl) or x.dtype not in _HALF:
         return _follow_layout(F.conv3d(x, weight, bias, st, pd, dl), x)
     _ensure_native(x.device)
-    with torch.cuda.device(x.device):
-        return _native.conv3d_fwd(x, weight.to(x.dtype), None if bias is None else bias.to(x.dtype), pd)
+    try:
+        with torch.cuda.device(x.device):
+            return _native.conv3d_fwd(x, weight.to(x.dtype), None if bias is None else bias.to(x.dtype), pd)
+    except _native.NativeUnsupported as e:
+        _fallback_warning("wmma_fwd", e)
+        return _follow_layout(F.conv3d(x, weight.to(x.dtype), None if bias is None else bias.to(x.dtype), st, pd,
+                                       dl), x)
 
 
 def wmma_dw(x, weight, go, stride=1, padding=0, dilation=1):
@@ -323,8 +368,12 @@ def wmma_dw(x, weight, go, stride=1, padding=0, dilation=1):
     if not _conv_native_ok(x, weight, st, pd, dl) or go.dtype not in _HALF or x.dtype != go.dtype:
         return torch.nn.grad.conv3d_weight(x.to(go.dtype), weight.shape, go.contiguous(), st, pd, dl, 1)
     _ensure_native(x.device)
-    with torch.cuda.device(x.device):
-        dw, _ = _native.conv3d_dw(x, go, weight.shape, pd, go.dtype)
+    try:
+        with torch.cuda.device(x.device):
+            dw, _ = _native.conv3d_dw(x, go, weight.shape, pd, go.dtype)
+    except _native.NativeUnsupported as e:
+        _fallback_warning("wmma_dw", e)
+        dw = torch.nn.grad.conv3d_weight(x, weight.shape, go.contiguous(), st, pd, dl, 1)
     return dw
 
 
@@ -336,8 +385,12 @@ def wmma_dx(x, weight, go, stride=1, padding=0, dilation=1):
         gx = torch.nn.grad.conv3d_input(x.shape, w, go.contiguous(), st, pd, dl, 1)
         return _follow_layout(gx, x)
     _ensure_native(x.device)
-    with torch.cuda.device(x.device):
-        return _native.conv3d_dx(go, weight.to(go.dtype), x.shape, pd, like=x)
+    try:
+        with torch.cuda.device(x.device):
+            return _native.conv3d_dx(go, weight.to(go.dtype), x.shape, pd, like=x)
+    except _native.NativeUnsupported as e:
+        _fallback_warning("wmma_dx", e)
+        return _stock_dx(x, weight, go, st, pd, dl)
 
 
 # ---------------------------------------------------------------------------
@@ -407,7 +460,10 @@ def _convt_native_ok(x, weight) -> bool:
         return False
     if int(x.shape[1]) != int(weight.shape[0]):
         return False
-    return _native_tensors_ok(x, weight)
+    if not _native_tensors_ok(x, weight):
+        return False
+    compute = x.dtype if x.dtype in _HALF else torch.float16
+    return _native.convt_plans_ok(x, weight.shape, compute)
 
 
 def transpose_k2s2_fwd(x, weight, bias=None):
@@ -430,6 +486,19 @@ def transpose_k2s2_dw(x, weight_shape, go, dw_dtype=None):
     return dw
 
 
+def _stock_convt_grads(x, weight, go, need_x, need_w):
+    """dX (x's layout) and dW (weight's dtype) of a k=2 s=2 ConvTranspose3d by PyTorch."""
+    with torch.enable_grad():
+        xr = x.detach().requires_grad_(need_x)
+        wr = weight.detach().to(go.dtype).requires_grad_(need_w)
+        y = F.conv_transpose3d(xr.to(go.dtype), wr, None, stride=2)
+        ins = [t for t, n in ((xr, need_x), (wr, need_w)) if n]
+        grads = list(torch.autograd.grad(y, ins, go))
+    gx = _follow_layout(grads.pop(0), x) if need_x else None
+    dw = grads.pop(0).to(weight.dtype) if need_w else None
+    return gx, dw
+
+
 class ConvTranspose3dWmmaFn(torch.autograd.Function):
     @staticmethod
     def forward(x, weight, bias):
@@ -438,7 +507,11 @@ class ConvTranspose3dWmmaFn(torch.autograd.Function):
             x = x.to(torch.float16)
             weight = weight.to(torch.float16)
             bias = None if bias is None else bias.to(torch.float16)
-        y = transpose_k2s2_fwd(x, weight, bias)
+        try:
+            y = transpose_k2s2_fwd(x, weight, bias)
+        except _native.NativeUnsupported as e:
+            _fallback_warning("ConvTranspose3d forward", e)
+            y = F.conv_transpose3d(x, weight.to(x.dtype), None if bias is None else bias.to(x.dtype), stride=2)
         if compute_dtype not in _HALF:
             y = y.to(compute_dtype)
         return y
@@ -462,14 +535,23 @@ class ConvTranspose3dWmmaFn(torch.autograd.Function):
         with torch.cuda.device(x.device):
             if need_x:
                 w_c = weight if weight.dtype == half else weight.to(half)
-                gx = _native.convt_dx(go, w_c, x.shape, like=x)
+                try:
+                    gx = _native.convt_dx(go, w_c, x.shape, like=x)
+                except _native.NativeUnsupported as e:
+                    _fallback_warning("ConvTranspose3d dX", e)
+                    gx, _ = _stock_convt_grads(x.to(half), w_c, go, True, False)
                 if gx.dtype != x.dtype:
                     gx = gx.to(x.dtype)
             if need_w or need_b:
                 x_c = x if x.dtype == half else x.to(half)
                 dw_dtype = torch.float32 if weight.dtype == torch.float32 else half
-                dw, db = _native.convt_dw(x_c, go, weight.shape, dw_dtype, want_db=need_b,
-                                          db_dtype=_db_dtype(ctx.bias_dtype, half))
+                try:
+                    dw, db = _native.convt_dw(x_c, go, weight.shape, dw_dtype, want_db=need_b,
+                                              db_dtype=_db_dtype(ctx.bias_dtype, half))
+                except _native.NativeUnsupported as e:
+                    _fallback_warning("ConvTranspose3d dW", e)
+                    _, dw = _stock_convt_grads(x_c, weight, go, False, True)
+                    db = go.float().sum(dim=(0, 2, 3, 4)) if need_b else None
                 dw = dw.to(weight.dtype) if need_w else None
                 if need_b and db.dtype != ctx.bias_dtype:
                     db = db.to(ctx.bias_dtype)
@@ -483,7 +565,9 @@ class ConvTranspose3dWmma(nn.ConvTranspose3d):
         if (output_size is not None or self.kernel_size != (2, 2, 2) or self.stride != (2, 2, 2)
                 or self.padding != (0, 0, 0) or self.output_padding != (0, 0, 0) or self.groups != 1
                 or self.dilation != (1, 1, 1) or self.padding_mode != "zeros" or not x.is_cuda
-                or not _wmma_hw() or not _convt_native_ok(x, self.weight)):
+                or not _wmma_hw()):
             return super().forward(x, output_size)
-        x, weight, bias = _autocast_args(x, self.weight, self.bias)
-        return ConvTranspose3dWmmaFn.apply(x, weight, bias)
+        xa, weight, bias = _autocast_args(x, self.weight, self.bias)
+        if not _convt_native_ok(xa, weight):
+            return super().forward(x, output_size)
+        return ConvTranspose3dWmmaFn.apply(xa, weight, bias)

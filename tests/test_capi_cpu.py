@@ -98,3 +98,48 @@ def test_dw_workspace_scales_with_problem(k, pad):
     small = lib.r3c_conv3d_dw_workspace(ctypes.byref(_desc(k=k, pad=pad, sp=(4, 4, 16))))
     big = lib.r3c_conv3d_dw_workspace(ctypes.byref(_desc(k=k, pad=pad, sp=(32, 64, 64))))
     assert 0 < small <= big <= (96 << 20) + (1 << 20)
+
+
+def _desc_strided(shape_x, shape_y, k, pad, channels_last=False, transpose=False):
+    """Descriptor with dense NCDHW (or NDHWC) strides computed from the shapes
+    (no tensor is allocated, so samples past 1 GiB cost nothing here)."""
+    def st(s):
+        n, c, d, h, w = s
+        return (c * d * h * w, 1, h * w * c, w * c, c) if channels_last else (c * d * h * w, d * h * w, h * w, w, 1)
+    import torch
+    return _native.make_desc(shape_x, shape_y, k, (pad,) * 3, torch.bfloat16, st(shape_x), st(shape_y))
+
+
+@pytest.mark.parametrize("channels_last", [False, True], ids=["ncdhw", "ndhwc"])
+def test_workspace_query_rejects_samples_of_1gib(channels_last):
+    """A sample of 1 GiB or more needs offsets past the kernels' 32-bit buffer
+    ranges: every workspace query returns -1 for it (the caller falls back
+    before running anything), while the same layer at half the depth is
+    accepted."""
+    lib = _native.load()
+    big_x = (1, 64, 128, 256, 256)   # 2^30 bytes of bf16 per sample
+    ok_x = (1, 64, 64, 256, 256)
+    for xs, expect_ok in ((big_x, False), (ok_x, True)):
+        for k, pad in ((3, 1), (1, 0)):
+            d = _desc_strided(xs, (xs[0], 64) + xs[2:], k, pad, channels_last)
+            for name in ("fwd", "dx", "dw"):
+                v = getattr(lib, f"r3c_conv3d_{name}_workspace")(ctypes.byref(d))
+                assert (v >= 0) == expect_ok, (xs, k, name, v)
+        t = _desc_strided(xs, (xs[0], 8) + tuple(2 * v for v in xs[2:]), 2, 0, channels_last, transpose=True)
+        for name in ("fwd", "dx", "dw"):
+            v = getattr(lib, f"r3c_convt_k2s2_{name}_workspace")(ctypes.byref(t))
+            assert (v >= 0) == expect_ok, (xs, name, v)
+
+
+def test_plan_check_declines_1gib_sample_on_host():
+    """The Python predicate the autograd Functions use before a native forward
+    (conv_plans_ok) says no for the 1 GiB sample and yes at half its depth;
+    meta tensors carry the shapes and strides, nothing is allocated."""
+    import torch
+    big = torch.empty(1, 64, 128, 256, 256, dtype=torch.bfloat16, device="meta")
+    ok = torch.empty(1, 64, 64, 256, 256, dtype=torch.bfloat16, device="meta")
+    w = (64, 64, 3, 3, 3)
+    assert not _native.conv_plans_ok(big, w, (1, 1, 1), torch.bfloat16)
+    assert _native.conv_plans_ok(ok, w, (1, 1, 1), torch.bfloat16)
+    assert not _native.convt_plans_ok(big, (64, 8, 2, 2, 2), torch.bfloat16)
+    assert _native.convt_plans_ok(ok, (64, 8, 2, 2, 2), torch.bfloat16)
