@@ -113,6 +113,21 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
                       void* dw, int32_t dw_dtype, void* db, int32_t db_dtype,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Conv3d dW without a caller workspace -------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): r3c_conv3d_dw with the workspace taken from a static
+ * device array of the library (64 MiB, one per GPU, resident until the process
+ * ends) instead of an argument.  The caller still passes x, dy, dw and db.
+ * Allocates nothing (no hipMalloc / hipFree).  Returns R3C_UNSUPPORTED, with
+ * r3c_last_error() naming the bytes needed, when the pass needs more than the
+ * array holds (r3c_conv3d_dw_workspace > 64 MiB).  Every call on one GPU uses
+ * the same array and overwrites it (no part of it needs to start at zero):
+ * calls that overlap on one GPU (different streams or threads) race. */
+int32_t r3c_conv3d_dw_static(const r3c_conv_desc* desc, const void* x,
+                             const void* dy, void* dw, int32_t dw_dtype,
+                             void* db, int32_t db_dtype, void* stream);
+
 /* ---- ConvTranspose3d k=2 s=2 ------------------------------------------------
  * Replace transpose_k2s2_fwd / _dx / _dw (src/rdna4_conv3d/conv3d_wmma.py:
  * 1462-1542, kernels 793-1012) and db = go.sum (conv3d_wmma.py:1576).

@@ -1200,6 +1200,38 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
 std::mutex g_dev_mu;
 std::unordered_map<int, int> g_dev_ok;
 
+// Device address of `scratch` (below) on each device, looked up once per
+// device with that device current: every GPU holds its own copy of the array.
+std::mutex g_scratch_mu;
+std::unordered_map<int, void*> g_scratch_ptr;
+
+}  // namespace
+
+// Workspace of the allocation-free dW entry point r3c_conv3d_dw_static: a
+// file-scope device array, resident on every GPU the library runs on until the
+// process ends.  In host code `scratch` names a host-side stand-in, never a
+// device address: only the pointer from hipGetSymbolAddress is passed on.
+constexpr int64_t kStaticScratchBytes = 64ll << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+int static_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(R3C_HIP_ERROR, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(R3C_HIP_ERROR, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    it = g_scratch_ptr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return R3C_OK;
+}
+
 }  // namespace
 }  // namespace r3c
 
@@ -1249,6 +1281,22 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* d, const void* x, const void* dy, voi
   if (rc) return rc;
   return run_wgrad(d, false, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
 }
+
+int32_t r3c_conv3d_dw_static(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype,
+                             void* db, int32_t db_dtype, void* stream) {
+  int rc = validate(d, false);
+  if (rc) return rc;
+  const int64_t need = wgrad_ws(d, false);
+  if (need < 0) return fail(R3C_UNSUPPORTED, "no weight-gradient plan for this descriptor");
+  if (need > kStaticScratchBytes)
+    return fail(R3C_UNSUPPORTED, "r3c_conv3d_dw_static: the pass needs %lld bytes of scratch, the static scratch holds %lld",
+                (long long)need, (long long)kStaticScratchBytes);
+  void* ws = nullptr;
+  rc = static_scratch(&ws);
+  if (rc) return rc;
+  return run_wgrad(d, false, x, dy, dw, dw_dtype, db, db_dtype, ws, kStaticScratchBytes, stream);
+}
+
 
 int32_t r3c_convt_k2s2_fwd(const r3c_conv_desc* d, const void* x, const void* w, const void* bias, void* y, void* ws,
                            int64_t ws_bytes, void* stream) {

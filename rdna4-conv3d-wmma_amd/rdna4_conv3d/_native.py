@@ -88,6 +88,8 @@ def _bind(lib: ctypes.CDLL) -> None:
         f = getattr(lib, f"r3c_{name}")
         f.restype = I32
         f.argtypes = [D, P, P, P, I32, P, I32, P, I64, P]
+    lib.r3c_conv3d_dw_static.restype = I32
+    lib.r3c_conv3d_dw_static.argtypes = [D, P, P, P, I32, P, I32, P]
     lib.r3c_timing_enable.restype = I32
     lib.r3c_timing_enable.argtypes = [I32]
     lib.r3c_timing_set_tag.restype = None
