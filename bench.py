@@ -27,8 +27,10 @@ Also reported on the same JSON line:
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
   unet3d        BASELINE config 5: ms per AMP training step (and per sample) of the
-                base=24 UNet3D at batch 4 built with this package's layers, the same
-                with stock nn.Conv3d / nn.ConvTranspose3d, and the largest loss gap;
+                base=24 UNet3D at batch 4 built with this package's layers, with its
+                fused BatchNorm + ReLU too, and with stock nn.Conv3d /
+                nn.ConvTranspose3d; the largest loss gaps over 40 steps against
+                stock, and stock's own spread (the batch in reversed order);
                 unet3d_base32 the same at base=32.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
@@ -122,20 +124,27 @@ def cpu_baseline(budget_s: float = 20.0):
     }
 
 
-def _unet_block(cin, cout, conv):
+def _unet_block(cin, cout, conv, bnrelu=None):
+    """Two (3x3x3 conv, BatchNorm, ReLU); `bnrelu(c)` builds one fused
+    BatchNorm + ReLU module in place of nn.BatchNorm3d(c), nn.ReLU().  Both
+    forms create their parameters in the same order, so a seeded build gives
+    the same initial weights either way."""
     import torch.nn as nn
-    return nn.Sequential(
-        conv(cin, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
-        conv(cout, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
-    )
+    if bnrelu is None:
+        return nn.Sequential(
+            conv(cin, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
+            conv(cout, cout, 3, padding=1), nn.BatchNorm3d(cout), nn.ReLU(inplace=True),
+        )
+    return nn.Sequential(conv(cin, cout, 3, padding=1), bnrelu(cout), conv(cout, cout, 3, padding=1), bnrelu(cout))
 
 
-def build_unet3d(conv, tr, base=24, cin=1, classes=2):
+def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None):
     """UNet3D of BASELINE config 5: 4 levels (base, 2, 4, 8 x base channels),
     two (3x3x3 conv + BatchNorm + ReLU) per block, MaxPool3d(2) down,
     ConvTranspose3d k2s2 up with skip concat, 1x1x1 head to `classes`.
     `conv` / `tr` are the Conv3d / ConvTranspose3d classes to build with (the
-    reference's factory pattern, benches/unet_e2e.py:13-32)."""
+    reference's factory pattern, benches/unet_e2e.py:13-32); `bnrelu`, if
+    given, builds the fused BatchNorm + ReLU modules."""
     import torch
     import torch.nn as nn
 
@@ -144,13 +153,14 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2):
     class UNet3D(nn.Module):
         def __init__(self):
             super().__init__()
-            self.enc = nn.ModuleList([_unet_block(cin, ch[0], conv), _unet_block(ch[0], ch[1], conv),
-                                      _unet_block(ch[1], ch[2], conv), _unet_block(ch[2], ch[3], conv)])
+            self.enc = nn.ModuleList([_unet_block(cin, ch[0], conv, bnrelu), _unet_block(ch[0], ch[1], conv, bnrelu),
+                                      _unet_block(ch[1], ch[2], conv, bnrelu), _unet_block(ch[2], ch[3], conv, bnrelu)])
             self.pool = nn.MaxPool3d(2)
             self.up = nn.ModuleList([tr(ch[3], ch[2], 2, stride=2), tr(ch[2], ch[1], 2, stride=2),
                                      tr(ch[1], ch[0], 2, stride=2)])
-            self.dec = nn.ModuleList([_unet_block(2 * ch[2], ch[2], conv), _unet_block(2 * ch[1], ch[1], conv),
-                                      _unet_block(2 * ch[0], ch[0], conv)])
+            self.dec = nn.ModuleList([_unet_block(2 * ch[2], ch[2], conv, bnrelu),
+                                      _unet_block(2 * ch[1], ch[1], conv, bnrelu),
+                                      _unet_block(2 * ch[0], ch[0], conv, bnrelu)])
             self.head = conv(ch[0], classes, 1)
 
         def forward(self, x):
@@ -219,7 +229,7 @@ def _rounded_layers():
     return RoundedConv3d, RoundedConvTranspose3d
 
 
-def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False):
+def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False, bnrelu=None):
     """AMP training of build_unet3d(conv, tr, base) on (x, labels):
     cross-entropy, Adam(lr=1e-3), autocast in `amp_dtype` (bf16 by default,
     BASELINE config 5; torch.float16 is the reference's protocol,
@@ -232,7 +242,7 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, chann
     import torch.nn as nn
     amp_dtype = amp_dtype or torch.bfloat16
     torch.manual_seed(1)
-    net = build_unet3d(conv, tr, base).to(x.device)
+    net = build_unet3d(conv, tr, base, bnrelu=bnrelu).to(x.device)
     if channels_last:
         net = net.to(memory_format=torch.channels_last_3d)
         x = x.contiguous(memory_format=torch.channels_last_3d)
@@ -341,17 +351,38 @@ def hbm_passes(layout: str, reps: int = 20):
 
 
 def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
-    """this package's layers vs stock nn.Conv3d / nn.ConvTranspose3d."""
+    """the UNet3D built with this package's layers (and, as
+    a second variant, with its fused BatchNorm + ReLU as well) against stock
+    nn.Conv3d / nn.ConvTranspose3d, AMP bf16.
+
+    Loss tracking is reported against the spread of stock itself: the same
+    stock model trained on the same batch with the sample order reversed (a
+    second correct bf16 computation of the same step: every sum over the batch
+    runs in another order).  The north star's |dloss| <= 1e-3 over 40 steps
+    sits below that spread."""
     import torch
     import torch.nn as nn
     from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
+    from rdna4_conv3d.fused import BatchNormReLU3d
     g = torch.Generator().manual_seed(0)
     x = torch.randn(batch, 1, 64, 128, 128, generator=g).cuda()
     labels = torch.randint(0, 2, (batch, 64, 128, 128), generator=torch.Generator().manual_seed(3)).cuda()
     ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
+    ms_f, loss_f = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup,
+                                bnrelu=BatchNormReLU3d)
+    torch.cuda.empty_cache()
     ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
+    rev = torch.arange(batch - 1, -1, -1, device=x.device)
+    _, loss_r = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x[rev].contiguous(), labels[rev].contiguous(),
+                             steps, warmup)
+    torch.cuda.empty_cache()
+    n40 = min(40, len(loss_s))
+
+    def gap(a, b):
+        return round(max(abs(u - v) for u, v in zip(a[:n40], b[:n40])), 6)
+
     return {
         "config": f"base={base} b{batch} x[{batch},1,64,128,128] AMP bf16, CrossEntropy, Adam lr 1e-3, NCDHW",
         "steps": steps,
@@ -360,10 +391,39 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
         "ms_per_sample": round(ms_w / batch, 3),
         "stock_ms_per_step": round(ms_s, 3),
         "speedup_vs_stock": round(ms_s / ms_w, 3),
-        "max_abs_dloss": round(max(abs(a - b) for a, b in zip(loss_w, loss_s)), 6),
+        "fused_bn_ms_per_step": round(ms_f, 3),
+        "fused_bn_ms_per_sample": round(ms_f / batch, 3),
+        "fused_bn_speedup_vs_stock": round(ms_s / ms_f, 3),
+        "loss_steps_compared": n40,
+        "max_abs_dloss": gap(loss_w, loss_s),
+        "max_abs_dloss_fused_bn": gap(loss_f, loss_s),
+        "max_abs_dloss_stock_vs_stock_batch_reversed": gap(loss_r, loss_s),
         "final_loss": round(loss_w[-1], 6),
         "stock_final_loss": round(loss_s[-1], 6),
     }
+
+
+def unet_probe(name: str) -> int:
+    """Kernels of UNet3D training steps for a kernel trace (rocprofv3
+    --kernel-trace --stats): `unet<base>[_fused|_stock]` runs 3 warmup + 5 AMP
+    bf16 steps of BASELINE config 5 built with this package's layers (with its
+    fused BatchNorm + ReLU for _fused, stock layers for _stock)."""
+    import torch
+    import torch.nn as nn
+    from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
+    from rdna4_conv3d.fused import BatchNormReLU3d
+    stem, _, kind = name.partition("_")
+    base = int(stem[4:] or 24)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 1, 64, 128, 128, generator=g).cuda()
+    labels = torch.randint(0, 2, (4, 64, 128, 128), generator=torch.Generator().manual_seed(3)).cuda()
+    if kind == "stock":
+        ms, _ = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, 5, 3)
+    else:
+        ms, _ = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, 5, 3,
+                             bnrelu=BatchNormReLU3d if kind == "fused" else None)
+    print(f"probe {name}: {ms:.3f} ms/step", flush=True)
+    return 0
 
 
 def traffic_probe(name: str, layout: str) -> int:
@@ -417,7 +477,8 @@ def main() -> int:
     ap.add_argument("--no-hbm-passes", action="store_true", help="skip the k=1 / ConvTranspose3d passes")
     ap.add_argument("--probe", default=None, metavar="PASS",
                     help="traffic probe for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB Tensor.copy_ (the "
-                         "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd; exits")
+                         "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd; or "
+                         "unet24[_fused|_stock]: 8 UNet3D training steps for a kernel trace; exits")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="diagnostic: time the step without the per-launch event hook (no roofline/passes)")
     args = ap.parse_args()
@@ -446,6 +507,8 @@ def main() -> int:
     def L(t):
         return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
 
+    if args.probe and args.probe.startswith("unet"):
+        return unet_probe(args.probe)
     if args.probe:
         return traffic_probe(args.probe, layout)
 

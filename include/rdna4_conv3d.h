@@ -147,13 +147,56 @@ int32_t r3c_convt_k2s2_dw(const r3c_conv_desc* desc, const void* x,
                           int32_t db_dtype, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* ---- BatchNorm3d + ReLU (the conv -> BN -> ReLU block) ----------------------
+ * No counterpart in the reference package: it replaces the nn.BatchNorm3d +
+ * nn.ReLU pair of the UNet3D block the reference accelerates
+ * (benches/unet_e2e.py:13-21; examples/drop_in_unet.py), with PyTorch's
+ * training-mode semantics (batch statistics, biased variance for the
+ * normalisation, running statistics updated with the unbiased variance and
+ * `momentum`) or evaluation semantics (running statistics).
+ * Tensors are [n, c, positions] with each (sample, channel) plane of `s`
+ * positions contiguous (NCDHW); element strides of sample and channel are
+ * given per tensor.  s, the strides and every pointer must allow 16-byte
+ * vectors (s and strides multiples of 8 elements for 16-bit types, 4 for
+ * fp32; 16-byte aligned pointers), else R3C_UNSUPPORTED.  gamma / beta may be
+ * NULL (no affine transform); running_mean / running_var may be NULL in
+ * training mode (no running statistics).  Every reduction has a fixed order:
+ * results are bitwise reproducible. */
+typedef struct r3c_bn_desc {
+  int32_t dtype;              /* R3C_F16, R3C_BF16 or R3C_F32: y, z, dz, dy */
+  int32_t n, c;
+  int64_t s;                  /* positions per (sample, channel) plane */
+  int64_t y_strides[2];       /* sample, channel strides of y (elements) */
+  int64_t g_strides[2];       /* of dz (backward) */
+  int64_t o_strides[2];       /* of z (forward) or dy (backward) */
+  int32_t training;           /* 1: batch statistics; 0: running statistics */
+  float eps, momentum;        /* momentum: weight of the batch statistics in the running update */
+} r3c_bn_desc;
+
+/* Workspace for both passes (partial sums and per-channel coefficients). */
+int64_t r3c_bn_relu_workspace(const r3c_bn_desc* desc);
+/* z = relu(batchnorm(y)); save_mean / save_invstd [c] receive the statistics
+ * used (batch or running), which the backward takes back. */
+int32_t r3c_bn_relu_fwd(const r3c_bn_desc* desc, const void* y, const float* gamma,
+                        const float* beta, float* running_mean, float* running_var,
+                        void* z, float* save_mean, float* save_invstd,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+/* dy, dgamma, dbeta (either may be NULL) from dz = dL/dz and the forward's y
+ * and saved statistics. */
+int32_t r3c_bn_relu_bwd(const r3c_bn_desc* desc, const void* dz, const void* y,
+                        const float* gamma, const float* beta,
+                        const float* save_mean, const float* save_invstd,
+                        void* dy, float* dgamma, float* dbeta,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- Kernel timing hook (measurement only) ----------------------------------
  * No counterpart in the reference (its benches time whole calls with
  * time.perf_counter, benches/isolated.py:26-34).  While enabled, each kernel
  * launch is bracketed by HIP events on its own launch stream and tagged with
  * the calling thread's current tag and a kernel family
  * (0 weight pack, 1 row kernel, 2 weight-gradient kernel, 3 split reduce,
- * 4 NCDHW-to-NDHWC copy, 5 row-kernel split-K epilogue pass).
+ * 4 NCDHW-to-NDHWC copy, 5 row-kernel split-K epilogue pass, 6 BatchNorm +
+ * ReLU pass: all kernels of one forward or backward call).
  * r3c_timing_collect waits for the recorded events, writes up to max_records
  * (tag, kind, milliseconds) triples, clears the records and returns how many
  * launches were recorded.  r3c_timing_filter limits recording to launches

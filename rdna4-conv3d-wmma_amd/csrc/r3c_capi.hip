@@ -117,7 +117,9 @@ int ok() {
 // caller's current tag and the kernel family; collect() waits for them and
 // returns the per-launch durations.
 // ---------------------------------------------------------------------------
-enum KernelKind { KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4, KIND_SPLIT_EPI = 5 };
+enum KernelKind {
+  KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4, KIND_SPLIT_EPI = 5, KIND_BN = 6
+};
 
 struct TimingRec {
   int tag, kind;
@@ -1172,6 +1174,53 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
 // Workspace queries: -1 when the descriptor is invalid or no plan can run it
 // (the caller then falls back).  The size covers every plan the launch may
 // take for this descriptor, whatever the pointers' alignment.
+// ---------------------------------------------------------------------------
+// BatchNorm + ReLU
+// ---------------------------------------------------------------------------
+int bn_validate(const r3c_bn_desc* d) {
+  if (!d) return fail(R3C_INVALID, "descriptor is NULL");
+  if (d->dtype != R3C_F16 && d->dtype != R3C_BF16 && d->dtype != R3C_F32)
+    return fail(R3C_UNSUPPORTED, "BatchNorm: dtype %d is not fp16, bf16 or fp32", d->dtype);
+  if (d->n < 1 || d->c < 1 || d->s < 1) return fail(R3C_INVALID, "BatchNorm: every dimension must be >= 1");
+  if (d->n > 65535 || d->c > 65535) return fail(R3C_UNSUPPORTED, "BatchNorm: n and c must be <= 65535");
+  const int vec = d->dtype == R3C_F32 ? 4 : 8;
+  if (d->s % vec) return fail(R3C_UNSUPPORTED, "BatchNorm: positions per plane must be a multiple of %d", vec);
+  const int64_t* st[3] = {d->y_strides, d->g_strides, d->o_strides};
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 2; ++j)
+      if (st[i][j] < 0 || st[i][j] % vec) return fail(R3C_UNSUPPORTED, "BatchNorm: strides must be multiples of %d", vec);
+  if ((d->s + kBnChunk - 1) / kBnChunk >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "BatchNorm: plane too large");
+  return R3C_OK;
+}
+
+int64_t bn_ws(const r3c_bn_desc* d) {
+  const int64_t nchunk = (d->s + kBnChunk - 1) / kBnChunk;
+  return align256((int64_t)d->n * nchunk * d->c * 2 * 4) + align256((int64_t)d->c * 4 * 4);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+BnArgs bn_args(const r3c_bn_desc* d, void* ws) {
+  BnArgs a;
+  memset(&a, 0, sizeof a);
+  a.S = d->s;
+  a.N = d->n;
+  a.C = d->c;
+  a.nchunk = (int32_t)((d->s + kBnChunk - 1) / kBnChunk);
+  a.training = d->training ? 1 : 0;
+  a.eps = d->eps;
+  a.momentum = d->momentum;
+  a.sn = d->y_strides[0];
+  a.sc = d->y_strides[1];
+  a.gn = d->g_strides[0];
+  a.gc = d->g_strides[1];
+  a.on = d->o_strides[0];
+  a.oc = d->o_strides[1];
+  a.part = static_cast<float*>(ws);
+  a.coef = reinterpret_cast<float*>(static_cast<char*>(ws) + align256((int64_t)d->n * a.nchunk * d->c * 2 * 4));
+  return a;
+}
+
 int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   RowPlan p;
@@ -1280,6 +1329,75 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* d, const void* x, const void* dy, voi
   int rc = validate(d, false);
   if (rc) return rc;
   return run_wgrad(d, false, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
+}
+
+int64_t r3c_bn_relu_workspace(const r3c_bn_desc* d) {
+  if (bn_validate(d) != R3C_OK) return -1;
+  return bn_ws(d);
+}
+
+int32_t r3c_bn_relu_fwd(const r3c_bn_desc* d, const void* y, const float* gamma, const float* beta,
+                        float* running_mean, float* running_var, void* z, float* save_mean, float* save_invstd,
+                        void* ws, int64_t ws_bytes, void* stream) {
+  int rc = bn_validate(d);
+  if (rc) return rc;
+  if (!y || !z || !save_mean || !save_invstd || !ws) return fail(R3C_INVALID, "NULL pointer");
+  if (!d->training && (!running_mean || !running_var))
+    return fail(R3C_INVALID, "BatchNorm: evaluation needs the running statistics");
+  if ((running_mean == nullptr) != (running_var == nullptr))
+    return fail(R3C_INVALID, "BatchNorm: running_mean and running_var go together");
+  if (ws_bytes < bn_ws(d))
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)bn_ws(d));
+  if (!aligned16(y) || !aligned16(z)) return fail(R3C_UNSUPPORTED, "BatchNorm needs 16-byte aligned tensors");
+  rc = check_device();
+  if (rc) return rc;
+  BnArgs a = bn_args(d, ws);
+  a.y = y;
+  a.out = z;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.running_mean = running_mean;
+  a.running_var = running_var;
+  a.save_mean = save_mean;
+  a.save_invstd = save_invstd;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    TimedLaunch tl(KIND_BN, s);
+    launch_bn_relu_fwd(d->dtype, a, s);
+    tl.end();
+  }
+  return check_launch("BatchNorm + ReLU forward");
+}
+
+int32_t r3c_bn_relu_bwd(const r3c_bn_desc* d, const void* dz, const void* y, const float* gamma, const float* beta,
+                        const float* save_mean, const float* save_invstd, void* dy, float* dgamma, float* dbeta,
+                        void* ws, int64_t ws_bytes, void* stream) {
+  int rc = bn_validate(d);
+  if (rc) return rc;
+  if (!dz || !y || !dy || !save_mean || !save_invstd || !ws) return fail(R3C_INVALID, "NULL pointer");
+  if (ws_bytes < bn_ws(d))
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)bn_ws(d));
+  if (!aligned16(dz) || !aligned16(y) || !aligned16(dy))
+    return fail(R3C_UNSUPPORTED, "BatchNorm needs 16-byte aligned tensors");
+  rc = check_device();
+  if (rc) return rc;
+  BnArgs a = bn_args(d, ws);
+  a.y = y;
+  a.dz = dz;
+  a.out = dy;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.save_mean = const_cast<float*>(save_mean);
+  a.save_invstd = const_cast<float*>(save_invstd);
+  a.dgamma = dgamma;
+  a.dbeta = dbeta;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    TimedLaunch tl(KIND_BN, s);
+    launch_bn_relu_bwd(d->dtype, a, s);
+    tl.end();
+  }
+  return check_launch("BatchNorm + ReLU backward");
 }
 
 int32_t r3c_conv3d_dw_static(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype,

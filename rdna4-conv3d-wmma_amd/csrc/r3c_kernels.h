@@ -188,6 +188,32 @@ struct LayoutArgs {
   int32_t C, N;
 };
 
+// BatchNorm3d + ReLU on NCDHW planes (r3c_bn.hip).  Positions of a
+// (sample, channel) plane are contiguous; chunks of kBnChunk positions are the
+// unit of work and of the fixed-order partial sums.
+constexpr int kBnChunk = 16384;
+struct BnArgs {
+  const void* y;          // BN input
+  const void* dz;         // backward: gradient of the BN + ReLU output
+  void* out;              // forward: z; backward: dy
+  int64_t sn, sc;         // y sample / channel strides (elements)
+  int64_t gn, gc;         // dz strides
+  int64_t on, oc;         // out strides
+  int64_t S;              // positions per plane
+  int32_t N, C, nchunk, training;
+  float eps, momentum;
+  const float* gamma;     // may be null (no affine)
+  const float* beta;
+  float* running_mean;    // may be null (no running statistics)
+  float* running_var;
+  float* save_mean;       // [C] batch (or running) mean and invstd, written by the forward
+  float* save_invstd;
+  float* dgamma;          // backward outputs, may be null
+  float* dbeta;
+  float* part;            // [N * nchunk][C][2] partial results (workspace)
+  float* coef;            // [C][4] per-channel coefficients (workspace)
+};
+
 // Host launchers (return false when no instantiation matches).
 // `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
@@ -205,5 +231,9 @@ bool launch_pwdw(int dtype, int mode, int tr, int tc, int nj, const PwdwArgs& a,
 // Register-direct ConvTranspose dX (rb 1 or 2 row blocks per workgroup).
 bool launch_t2dx(int dtype, int rb, const T2dxArgs& a, size_t lds, hipStream_t stream);
 void launch_t2dx_pack(const T2dxPackArgs& a, hipStream_t stream);
+// BatchNorm + ReLU: forward (statistics or running statistics, then z) and
+// backward (sums, then dy); dtype 0 fp16, 1 bf16, 2 fp32 (the C ABI's codes).
+void launch_bn_relu_fwd(int dtype, const BnArgs& a, hipStream_t stream);
+void launch_bn_relu_bwd(int dtype, const BnArgs& a, hipStream_t stream);
 
 }  // namespace r3c

@@ -43,6 +43,19 @@ class ConvDesc(ctypes.Structure):
     ]
 
 
+class BnDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("n", ctypes.c_int32), ("c", ctypes.c_int32),
+        ("s", ctypes.c_int64),
+        ("y_strides", ctypes.c_int64 * 2),
+        ("g_strides", ctypes.c_int64 * 2),
+        ("o_strides", ctypes.c_int64 * 2),
+        ("training", ctypes.c_int32),
+        ("eps", ctypes.c_float), ("momentum", ctypes.c_float),
+    ]
+
+
 class NativeError(RuntimeError):
     """A native entry point returned R3C_INVALID or R3C_HIP_ERROR."""
 
@@ -88,6 +101,13 @@ def _bind(lib: ctypes.CDLL) -> None:
         f = getattr(lib, f"r3c_{name}")
         f.restype = I32
         f.argtypes = [D, P, P, P, I32, P, I32, P, I64, P]
+    B = ctypes.POINTER(BnDesc)
+    lib.r3c_bn_relu_workspace.restype = I64
+    lib.r3c_bn_relu_workspace.argtypes = [B]
+    lib.r3c_bn_relu_fwd.restype = I32
+    lib.r3c_bn_relu_fwd.argtypes = [B, P, P, P, P, P, P, P, P, P, I64, P]
+    lib.r3c_bn_relu_bwd.restype = I32
+    lib.r3c_bn_relu_bwd.argtypes = [B, P, P, P, P, P, P, P, P, P, P, I64, P]
     lib.r3c_conv3d_dw_static.restype = I32
     lib.r3c_conv3d_dw_static.argtypes = [D, P, P, P, I32, P, I32, P]
     lib.r3c_timing_enable.restype = I32
@@ -137,7 +157,7 @@ def device_supported(device_index: int) -> bool:
     return bool(load().r3c_device_supported(int(device_index)))
 
 
-KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout", "split_epilogue")
+KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout", "split_epilogue", "bn")
 
 
 def timing_enable(on: bool) -> None:
@@ -391,3 +411,70 @@ def convt_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, dw_dtype: torch.dt
                                _stream_handle(x.device))
     _check(lib, rc, "r3c_convt_k2s2_dw")
     return dw, db
+
+
+# ---------------------------------------------------------------------------
+# BatchNorm3d + ReLU (NCDHW planes)
+# ---------------------------------------------------------------------------
+def bn_plane_ok(t: torch.Tensor) -> bool:
+    """A 5-D tensor whose (sample, channel) planes are contiguous runs of D*H*W
+    positions, with sizes, strides and address the 16-byte kernels accept."""
+    if t.dim() != 5 or t.dtype not in _DTYPE_CODE:
+        return False
+    n, c, d, h, w = (int(v) for v in t.shape)
+    s = d * h * w
+    st = t.stride()
+    if not (st[4] == 1 and (w == 1 or st[3] == w) and (h == 1 or st[2] == h * w)):
+        return False
+    vec = 4 if t.dtype == torch.float32 else 8
+    return s % vec == 0 and st[0] % vec == 0 and st[1] % vec == 0 and t.data_ptr() % 16 == 0
+
+
+def _bn_desc(y: torch.Tensor, g: Optional[torch.Tensor], o: torch.Tensor, training: bool, eps: float,
+             momentum: float) -> BnDesc:
+    d = BnDesc()
+    d.dtype = _DTYPE_CODE[y.dtype]
+    d.n, d.c = int(y.shape[0]), int(y.shape[1])
+    d.s = int(y.shape[2] * y.shape[3] * y.shape[4])
+    d.y_strides[0], d.y_strides[1] = int(y.stride(0)), int(y.stride(1))
+    gg = g if g is not None else y
+    d.g_strides[0], d.g_strides[1] = int(gg.stride(0)), int(gg.stride(1))
+    d.o_strides[0], d.o_strides[1] = int(o.stride(0)), int(o.stride(1))
+    d.training = 1 if training else 0
+    d.eps = float(eps)
+    d.momentum = float(momentum)
+    return d
+
+
+def bn_relu_fwd(y: torch.Tensor, gamma, beta, running_mean, running_var, training: bool, momentum: float,
+                eps: float):
+    """(z, save_mean, save_invstd): z = relu(batchnorm(y)) in y's dtype, NCDHW."""
+    lib = load()
+    z = torch.empty(y.shape, device=y.device, dtype=y.dtype)
+    c = int(y.shape[1])
+    save_mean = torch.empty(c, device=y.device, dtype=torch.float32)
+    save_invstd = torch.empty(c, device=y.device, dtype=torch.float32)
+    d = _bn_desc(y, None, z, training, eps, momentum)
+    ws = _workspace(lib.r3c_bn_relu_workspace(ctypes.byref(d)), y.device, "r3c_bn_relu_fwd")
+    rc = lib.r3c_bn_relu_fwd(ctypes.byref(d), _ptr(y), _ptr(gamma), _ptr(beta), _ptr(running_mean),
+                             _ptr(running_var), _ptr(z), _ptr(save_mean), _ptr(save_invstd), _ptr(ws), ws.numel(),
+                             _stream_handle(y.device))
+    _check(lib, rc, "r3c_bn_relu_fwd")
+    return z, save_mean, save_invstd
+
+
+def bn_relu_bwd(dz: torch.Tensor, y: torch.Tensor, gamma, beta, save_mean, save_invstd, training: bool,
+                want_dgamma: bool, want_dbeta: bool):
+    """(dy, dgamma or None, dbeta or None) of z = relu(batchnorm(y))."""
+    lib = load()
+    dy = torch.empty(y.shape, device=y.device, dtype=y.dtype)
+    c = int(y.shape[1])
+    dgamma = torch.empty(c, device=y.device, dtype=torch.float32) if want_dgamma else None
+    dbeta = torch.empty(c, device=y.device, dtype=torch.float32) if want_dbeta else None
+    d = _bn_desc(y, dz, dy, training, 0.0, 0.0)
+    ws = _workspace(lib.r3c_bn_relu_workspace(ctypes.byref(d)), y.device, "r3c_bn_relu_bwd")
+    rc = lib.r3c_bn_relu_bwd(ctypes.byref(d), _ptr(dz), _ptr(y), _ptr(gamma), _ptr(beta), _ptr(save_mean),
+                             _ptr(save_invstd), _ptr(dy), _ptr(dgamma), _ptr(dbeta), _ptr(ws), ws.numel(),
+                             _stream_handle(y.device))
+    _check(lib, rc, "r3c_bn_relu_bwd")
+    return dy, dgamma, dbeta

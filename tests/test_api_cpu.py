@@ -109,3 +109,23 @@ def test_geometries_cpu_match_stock(k, pad):
     drop.load_state_dict(stock.state_dict())
     x = torch.randn(2, 3, 5, 6, 7)
     assert torch.equal(stock(x), drop(x))
+
+
+def test_bnrelu_on_cpu_is_batchnorm_then_relu():
+    """BatchNormReLU3d (native BatchNorm + ReLU on gfx950) keeps nn.BatchNorm3d's
+    parameters, buffers and semantics; on the CPU it is exactly BatchNorm3d + ReLU."""
+    import torch.nn.functional as F
+    from rdna4_conv3d.fused import BatchNormReLU3d
+    torch.manual_seed(0)
+    mod = BatchNormReLU3d(6, momentum=None)
+    ref = nn.BatchNorm3d(6, momentum=None)
+    ref.load_state_dict(mod.state_dict())
+    assert set(mod.state_dict()) == set(ref.state_dict())
+    x = torch.randn(2, 6, 3, 4, 5)
+    for _ in range(2):
+        torch.testing.assert_close(mod(x), F.relu(ref(x)), atol=0, rtol=0)
+    torch.testing.assert_close(mod.running_var, ref.running_var, atol=0, rtol=0)
+    assert int(mod.num_batches_tracked) == 2
+    mod.eval()
+    ref.eval()
+    torch.testing.assert_close(mod(x), F.relu(ref(x)), atol=0, rtol=0)

@@ -143,3 +143,30 @@ def test_plan_check_declines_1gib_sample_on_host():
     assert _native.conv_plans_ok(ok, w, (1, 1, 1), torch.bfloat16)
     assert not _native.convt_plans_ok(big, (64, 8, 2, 2, 2), torch.bfloat16)
     assert _native.convt_plans_ok(ok, (64, 8, 2, 2, 2), torch.bfloat16)
+
+
+def test_bn_workspace_query_validates_on_host():
+    """BatchNorm + ReLU descriptors: the workspace query accepts planes the
+    16-byte kernels take and returns -1 otherwise (the module then runs stock)."""
+    lib = _native.load()
+
+    def bn_desc(n, c, s, dtype, stride_c=None):
+        d = _native.BnDesc()
+        d.dtype, d.n, d.c, d.s = dtype, n, c, s
+        sc = s if stride_c is None else stride_c
+        d.y_strides[0] = d.g_strides[0] = d.o_strides[0] = c * sc
+        d.y_strides[1] = d.g_strides[1] = d.o_strides[1] = sc
+        d.training, d.eps, d.momentum = 1, 1e-5, 0.1
+        return d
+
+    ok = bn_desc(4, 24, 64 * 128 * 128, _native.R3C_BF16)
+    ws = lib.r3c_bn_relu_workspace(ctypes.byref(ok))
+    nchunk = -(-64 * 128 * 128 // 16384)
+    assert ws >= 4 * nchunk * 24 * 2 * 4 + 24 * 16
+    assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(2, 8, 12, _native.R3C_F32))) > 0      # 12 % 4 == 0
+    assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(2, 8, 12, _native.R3C_BF16))) == -1    # 12 % 8 != 0
+    assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(2, 8, 16, _native.R3C_BF16, 20))) == -1  # odd stride
+    assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(1, 70000, 16, _native.R3C_BF16))) == -1
+    assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(0, 8, 16, _native.R3C_BF16))) == -1
+    rc = lib.r3c_bn_relu_fwd(ctypes.byref(ok), None, None, None, None, None, None, None, None, None, 0, None)
+    assert rc == _native.R3C_INVALID
