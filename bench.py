@@ -138,13 +138,14 @@ def _unet_block(cin, cout, conv, bnrelu=None):
     return nn.Sequential(conv(cin, cout, 3, padding=1), bnrelu(cout), conv(cout, cout, 3, padding=1), bnrelu(cout))
 
 
-def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None):
+def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None):
     """UNet3D of BASELINE config 5: 4 levels (base, 2, 4, 8 x base channels),
     two (3x3x3 conv + BatchNorm + ReLU) per block, MaxPool3d(2) down,
     ConvTranspose3d k2s2 up with skip concat, 1x1x1 head to `classes`.
     `conv` / `tr` are the Conv3d / ConvTranspose3d classes to build with (the
     reference's factory pattern, benches/unet_e2e.py:13-32); `bnrelu`, if
-    given, builds the fused BatchNorm + ReLU modules."""
+    given, builds the fused BatchNorm + ReLU modules, `pool` the MaxPool3d(2)
+    module class (nn.MaxPool3d by default)."""
     import torch
     import torch.nn as nn
 
@@ -155,7 +156,7 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None):
             super().__init__()
             self.enc = nn.ModuleList([_unet_block(cin, ch[0], conv, bnrelu), _unet_block(ch[0], ch[1], conv, bnrelu),
                                       _unet_block(ch[1], ch[2], conv, bnrelu), _unet_block(ch[2], ch[3], conv, bnrelu)])
-            self.pool = nn.MaxPool3d(2)
+            self.pool = (pool or nn.MaxPool3d)(2)
             self.up = nn.ModuleList([tr(ch[3], ch[2], 2, stride=2), tr(ch[2], ch[1], 2, stride=2),
                                      tr(ch[1], ch[0], 2, stride=2)])
             self.dec = nn.ModuleList([_unet_block(2 * ch[2], ch[2], conv, bnrelu),
@@ -229,7 +230,8 @@ def _rounded_layers():
     return RoundedConv3d, RoundedConvTranspose3d
 
 
-def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False, bnrelu=None):
+def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False, bnrelu=None,
+                 pool=None):
     """AMP training of build_unet3d(conv, tr, base) on (x, labels):
     cross-entropy, Adam(lr=1e-3), autocast in `amp_dtype` (bf16 by default,
     BASELINE config 5; torch.float16 is the reference's protocol,
@@ -242,7 +244,7 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, chann
     import torch.nn as nn
     amp_dtype = amp_dtype or torch.bfloat16
     torch.manual_seed(1)
-    net = build_unet3d(conv, tr, base, bnrelu=bnrelu).to(x.device)
+    net = build_unet3d(conv, tr, base, bnrelu=bnrelu, pool=pool).to(x.device)
     if channels_last:
         net = net.to(memory_format=torch.channels_last_3d)
         x = x.contiguous(memory_format=torch.channels_last_3d)
@@ -352,8 +354,8 @@ def hbm_passes(layout: str, reps: int = 20):
 
 def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     """the UNet3D built with this package's layers (and, as
-    a second variant, with its fused BatchNorm + ReLU as well) against stock
-    nn.Conv3d / nn.ConvTranspose3d, AMP bf16.
+    a second variant, with its fused BatchNorm + ReLU and MaxPool3d(2) as
+    well) against stock nn.Conv3d / nn.ConvTranspose3d, AMP bf16.
 
     Loss tracking is reported against the spread of stock itself: the same
     stock model trained on the same batch with the sample order reversed (a
@@ -363,14 +365,14 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     import torch
     import torch.nn as nn
     from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
-    from rdna4_conv3d.fused import BatchNormReLU3d
+    from rdna4_conv3d.fused import BatchNormReLU3d, MaxPool3dWmma
     g = torch.Generator().manual_seed(0)
     x = torch.randn(batch, 1, 64, 128, 128, generator=g).cuda()
     labels = torch.randint(0, 2, (batch, 64, 128, 128), generator=torch.Generator().manual_seed(3)).cuda()
     ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
     ms_f, loss_f = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup,
-                                bnrelu=BatchNormReLU3d)
+                                bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma)
     torch.cuda.empty_cache()
     ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
@@ -391,12 +393,13 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
         "ms_per_sample": round(ms_w / batch, 3),
         "stock_ms_per_step": round(ms_s, 3),
         "speedup_vs_stock": round(ms_s / ms_w, 3),
-        "fused_bn_ms_per_step": round(ms_f, 3),
-        "fused_bn_ms_per_sample": round(ms_f / batch, 3),
-        "fused_bn_speedup_vs_stock": round(ms_s / ms_f, 3),
+        "all_native_layers": "Conv3dWmma, ConvTranspose3dWmma, BatchNormReLU3d, MaxPool3dWmma",
+        "all_native_ms_per_step": round(ms_f, 3),
+        "all_native_ms_per_sample": round(ms_f / batch, 3),
+        "all_native_speedup_vs_stock": round(ms_s / ms_f, 3),
         "loss_steps_compared": n40,
         "max_abs_dloss": gap(loss_w, loss_s),
-        "max_abs_dloss_fused_bn": gap(loss_f, loss_s),
+        "max_abs_dloss_all_native": gap(loss_f, loss_s),
         "max_abs_dloss_stock_vs_stock_batch_reversed": gap(loss_r, loss_s),
         "final_loss": round(loss_w[-1], 6),
         "stock_final_loss": round(loss_s[-1], 6),
@@ -407,11 +410,12 @@ def unet_probe(name: str) -> int:
     """Kernels of UNet3D training steps for a kernel trace (rocprofv3
     --kernel-trace --stats): `unet<base>[_fused|_stock]` runs 3 warmup + 5 AMP
     bf16 steps of BASELINE config 5 built with this package's layers (with its
-    fused BatchNorm + ReLU for _fused, stock layers for _stock)."""
+    BatchNorm + ReLU and MaxPool3d(2) as well for _fused, stock layers for
+    _stock)."""
     import torch
     import torch.nn as nn
     from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
-    from rdna4_conv3d.fused import BatchNormReLU3d
+    from rdna4_conv3d.fused import BatchNormReLU3d, MaxPool3dWmma
     stem, _, kind = name.partition("_")
     base = int(stem[4:] or 24)
     g = torch.Generator().manual_seed(0)
@@ -421,7 +425,8 @@ def unet_probe(name: str) -> int:
         ms, _ = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, 5, 3)
     else:
         ms, _ = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, 5, 3,
-                             bnrelu=BatchNormReLU3d if kind == "fused" else None)
+                             bnrelu=BatchNormReLU3d if kind == "fused" else None,
+                             pool=MaxPool3dWmma if kind == "fused" else None)
     print(f"probe {name}: {ms:.3f} ms/step", flush=True)
     return 0
 

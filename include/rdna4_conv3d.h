@@ -189,6 +189,29 @@ int32_t r3c_bn_relu_bwd(const r3c_bn_desc* desc, const void* dz, const void* y,
                         void* dy, float* dgamma, float* dbeta,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- MaxPool3d(kernel 2, stride 2) ------------------------------------------
+ * No counterpart in the reference package: it replaces nn.MaxPool3d(2) of the
+ * UNet3D down path (benches/unet_e2e.py:27-37) with the semantics of
+ * PyTorch's CPU kernel (the first maximum of each 2x2x2 window in (kd, kh, kw)
+ * order; NaN propagates; an all -inf window picks its first element).
+ * The forward also writes a one-byte index per output (kd*4 + kh*2 + kw)
+ * that the backward uses; idx is [n][c][d/2][h/2][w/2]
+ * contiguous.  Tensors are [n, c, d, h, w] with dense (d, h, w) planes and the
+ * given sample / channel strides; d and h must be even and w a multiple of 8,
+ * x / dx strides multiples of 8 elements (4 for fp32), y / dy strides
+ * multiples of 4, x, y, dx, dy 16-byte and idx 4-byte aligned, else
+ * R3C_UNSUPPORTED.  The backward writes every element of dx. */
+typedef struct r3c_pool_desc {
+  int32_t dtype;              /* R3C_F16, R3C_BF16 or R3C_F32 */
+  int32_t n, c, d, h, w;      /* input (x / dx) dims */
+  int64_t x_strides[2];       /* sample, channel strides of x / dx (elements) */
+  int64_t y_strides[2];       /* of y / dy */
+} r3c_pool_desc;
+int32_t r3c_maxpool2_fwd(const r3c_pool_desc* desc, const void* x, void* y,
+                         uint8_t* idx, void* stream);
+int32_t r3c_maxpool2_bwd(const r3c_pool_desc* desc, const void* dy,
+                         const uint8_t* idx, void* dx, void* stream);
+
 /* ---- Kernel timing hook (measurement only) ----------------------------------
  * No counterpart in the reference (its benches time whole calls with
  * time.perf_counter, benches/isolated.py:26-34).  While enabled, each kernel
@@ -196,7 +219,7 @@ int32_t r3c_bn_relu_bwd(const r3c_bn_desc* desc, const void* dz, const void* y,
  * the calling thread's current tag and a kernel family
  * (0 weight pack, 1 row kernel, 2 weight-gradient kernel, 3 split reduce,
  * 4 NCDHW-to-NDHWC copy, 5 row-kernel split-K epilogue pass, 6 BatchNorm +
- * ReLU pass: all kernels of one forward or backward call).
+ * ReLU pass: all kernels of one forward or backward call, 7 MaxPool3d pass).
  * r3c_timing_collect waits for the recorded events, writes up to max_records
  * (tag, kind, milliseconds) triples, clears the records and returns how many
  * launches were recorded.  r3c_timing_filter limits recording to launches

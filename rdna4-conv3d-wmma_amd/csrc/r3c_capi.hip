@@ -118,7 +118,8 @@ int ok() {
 // returns the per-launch durations.
 // ---------------------------------------------------------------------------
 enum KernelKind {
-  KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4, KIND_SPLIT_EPI = 5, KIND_BN = 6
+  KIND_PACK = 0, KIND_ROW = 1, KIND_WGRAD = 2, KIND_REDUCE = 3, KIND_LAYOUT = 4, KIND_SPLIT_EPI = 5, KIND_BN = 6,
+  KIND_POOL = 7
 };
 
 struct TimingRec {
@@ -1221,6 +1222,41 @@ BnArgs bn_args(const r3c_bn_desc* d, void* ws) {
   return a;
 }
 
+// ---------------------------------------------------------------------------
+// MaxPool3d(2)
+// ---------------------------------------------------------------------------
+int pool_setup(const r3c_pool_desc* d, PoolArgs& a) {
+  if (!d) return fail(R3C_INVALID, "descriptor is NULL");
+  if (d->dtype != R3C_F16 && d->dtype != R3C_BF16 && d->dtype != R3C_F32)
+    return fail(R3C_UNSUPPORTED, "MaxPool3d: dtype %d is not fp16, bf16 or fp32", d->dtype);
+  if (d->n < 1 || d->c < 1 || d->d < 2 || d->h < 2 || d->w < 8) return fail(R3C_UNSUPPORTED, "MaxPool3d: too small");
+  if (d->d % 2 || d->h % 2 || d->w % 8) return fail(R3C_UNSUPPORTED, "MaxPool3d: d, h must be even and w a multiple of 8");
+  // x / dx move as 16-byte vectors of 8 (fp32: 4) elements, y / dy as 4 elements.
+  const int vec = d->dtype == R3C_F32 ? 4 : 8;
+  for (int j = 0; j < 2; ++j) {
+    if (d->x_strides[j] < 0 || d->x_strides[j] % vec)
+      return fail(R3C_UNSUPPORTED, "MaxPool3d: x strides must be multiples of %d", vec);
+    if (d->y_strides[j] < 0 || d->y_strides[j] % 4)
+      return fail(R3C_UNSUPPORTED, "MaxPool3d: y strides must be multiples of 4");
+  }
+  memset(&a, 0, sizeof a);
+  a.n = d->n;
+  a.c = d->c;
+  a.d = d->d;
+  a.h = d->h;
+  a.w = d->w;
+  a.od = d->d / 2;
+  a.oh = d->h / 2;
+  a.ow = d->w / 2;
+  a.xs0 = d->x_strides[0];
+  a.xs1 = d->x_strides[1];
+  a.ys0 = d->y_strides[0];
+  a.ys1 = d->y_strides[1];
+  if ((int64_t)a.n * a.c * a.od * a.oh * (a.ow / 4) >= (1ll << 31))
+    return fail(R3C_UNSUPPORTED, "MaxPool3d: more than 2^31 threads");
+  return R3C_OK;
+}
+
 int64_t fwd_ws(const r3c_conv_desc* d, int op, bool transpose) {
   if (validate(d, transpose) != R3C_OK) return -1;
   RowPlan p;
@@ -1398,6 +1434,48 @@ int32_t r3c_bn_relu_bwd(const r3c_bn_desc* d, const void* dz, const void* y, con
     tl.end();
   }
   return check_launch("BatchNorm + ReLU backward");
+}
+
+int32_t r3c_maxpool2_fwd(const r3c_pool_desc* d, const void* x, void* y, uint8_t* idx, void* stream) {
+  PoolArgs a;
+  int rc = pool_setup(d, a);
+  if (rc) return rc;
+  if (!x || !y || !idx) return fail(R3C_INVALID, "NULL pointer");
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 15) || (reinterpret_cast<uintptr_t>(idx) & 3))
+    return fail(R3C_UNSUPPORTED, "MaxPool3d needs 16-byte aligned tensors");
+  rc = check_device();
+  if (rc) return rc;
+  a.x = x;
+  a.y = y;
+  a.idx = idx;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    TimedLaunch tl(KIND_POOL, s);
+    launch_maxpool2_fwd(d->dtype, a, s);
+    tl.end();
+  }
+  return check_launch("MaxPool3d forward");
+}
+
+int32_t r3c_maxpool2_bwd(const r3c_pool_desc* d, const void* dy, const uint8_t* idx, void* dx, void* stream) {
+  PoolArgs a;
+  int rc = pool_setup(d, a);
+  if (rc) return rc;
+  if (!dy || !idx || !dx) return fail(R3C_INVALID, "NULL pointer");
+  if (!aligned16(dx) || (reinterpret_cast<uintptr_t>(dy) & 15) || (reinterpret_cast<uintptr_t>(idx) & 3))
+    return fail(R3C_UNSUPPORTED, "MaxPool3d needs 16-byte aligned tensors");
+  rc = check_device();
+  if (rc) return rc;
+  a.dy = dy;
+  a.dx = dx;
+  a.idx = const_cast<uint8_t*>(idx);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    TimedLaunch tl(KIND_POOL, s);
+    launch_maxpool2_bwd(d->dtype, a, s);
+    tl.end();
+  }
+  return check_launch("MaxPool3d backward");
 }
 
 int32_t r3c_conv3d_dw_static(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype,

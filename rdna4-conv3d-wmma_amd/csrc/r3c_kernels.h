@@ -214,6 +214,19 @@ struct BnArgs {
   float* coef;            // [C][4] per-channel coefficients (workspace)
 };
 
+// MaxPool3d(2, stride 2) on NCDHW planes (r3c_pool.hip).  Even d, h, w with
+// w % 8 == 0: every input element belongs to exactly one window.
+struct PoolArgs {
+  const void* x;          // forward input
+  void* y;                // forward output
+  const void* dy;         // backward: gradient of y
+  void* dx;               // backward: gradient of x (every element written)
+  uint8_t* idx;           // [n][c][od][oh][ow]: kd * 4 + kh * 2 + kw of the window maximum
+  int64_t xs0, xs1;       // x / dx sample and channel strides (elements; planes dense)
+  int64_t ys0, ys1;       // y / dy sample and channel strides
+  int32_t n, c, d, h, w, od, oh, ow;
+};
+
 // Host launchers (return false when no instantiation matches).
 // `cus`: compute units of the device; the grid is cus x resident workgroups per CU.
 bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, int cus, size_t lds_bytes,
@@ -235,5 +248,8 @@ void launch_t2dx_pack(const T2dxPackArgs& a, hipStream_t stream);
 // backward (sums, then dy); dtype 0 fp16, 1 bf16, 2 fp32 (the C ABI's codes).
 void launch_bn_relu_fwd(int dtype, const BnArgs& a, hipStream_t stream);
 void launch_bn_relu_bwd(int dtype, const BnArgs& a, hipStream_t stream);
+// MaxPool3d(2): forward (y, idx) and backward (dx); dtype as the C ABI's codes.
+void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);
+void launch_maxpool2_bwd(int dtype, const PoolArgs& a, hipStream_t stream);
 
 }  // namespace r3c

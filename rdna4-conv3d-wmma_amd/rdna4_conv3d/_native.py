@@ -56,6 +56,16 @@ class BnDesc(ctypes.Structure):
     ]
 
 
+class PoolDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("n", ctypes.c_int32), ("c", ctypes.c_int32), ("d", ctypes.c_int32), ("h", ctypes.c_int32),
+        ("w", ctypes.c_int32),
+        ("x_strides", ctypes.c_int64 * 2),
+        ("y_strides", ctypes.c_int64 * 2),
+    ]
+
+
 class NativeError(RuntimeError):
     """A native entry point returned R3C_INVALID or R3C_HIP_ERROR."""
 
@@ -108,6 +118,11 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_bn_relu_fwd.argtypes = [B, P, P, P, P, P, P, P, P, P, I64, P]
     lib.r3c_bn_relu_bwd.restype = I32
     lib.r3c_bn_relu_bwd.argtypes = [B, P, P, P, P, P, P, P, P, P, P, I64, P]
+    Q = ctypes.POINTER(PoolDesc)
+    lib.r3c_maxpool2_fwd.restype = I32
+    lib.r3c_maxpool2_fwd.argtypes = [Q, P, P, P, P]
+    lib.r3c_maxpool2_bwd.restype = I32
+    lib.r3c_maxpool2_bwd.argtypes = [Q, P, P, P, P]
     lib.r3c_conv3d_dw_static.restype = I32
     lib.r3c_conv3d_dw_static.argtypes = [D, P, P, P, I32, P, I32, P]
     lib.r3c_timing_enable.restype = I32
@@ -157,7 +172,7 @@ def device_supported(device_index: int) -> bool:
     return bool(load().r3c_device_supported(int(device_index)))
 
 
-KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout", "split_epilogue", "bn")
+KERNEL_KINDS = ("pack", "row", "wgrad", "reduce", "layout", "split_epilogue", "bn", "pool")
 
 
 def timing_enable(on: bool) -> None:
@@ -478,3 +493,51 @@ def bn_relu_bwd(dz: torch.Tensor, y: torch.Tensor, gamma, beta, save_mean, save_
                              _stream_handle(y.device))
     _check(lib, rc, "r3c_bn_relu_bwd")
     return dy, dgamma, dbeta
+
+
+# ---------------------------------------------------------------------------
+# MaxPool3d(2)
+# ---------------------------------------------------------------------------
+def pool_ok(t: torch.Tensor) -> bool:
+    """A tensor the MaxPool3d(2) kernels take: dense (d, h, w) planes, even d
+    and h, w a multiple of 8, strides and address allowing 16-byte vectors."""
+    if t.dim() != 5 or t.dtype not in _DTYPE_CODE:
+        return False
+    n, c, d, h, w = (int(v) for v in t.shape)
+    st = t.stride()
+    if not (st[4] == 1 and st[3] == w and st[2] == h * w):
+        return False
+    vec = 4 if t.dtype == torch.float32 else 8
+    return (d % 2 == 0 and h % 2 == 0 and w % 8 == 0 and st[0] % vec == 0 and st[1] % vec == 0
+            and t.data_ptr() % 16 == 0)
+
+
+def _pool_desc(x_shape, x_strides, y_strides, dtype) -> PoolDesc:
+    d = PoolDesc()
+    d.dtype = _DTYPE_CODE[dtype]
+    d.n, d.c, d.d, d.h, d.w = (int(v) for v in x_shape)
+    d.x_strides[0], d.x_strides[1] = int(x_strides[0]), int(x_strides[1])
+    d.y_strides[0], d.y_strides[1] = int(y_strides[0]), int(y_strides[1])
+    return d
+
+
+def maxpool2_fwd(x: torch.Tensor):
+    """(y, idx): MaxPool3d(2) of x and the one-byte window index of each maximum."""
+    lib = load()
+    n, c, d, h, w = (int(v) for v in x.shape)
+    y = torch.empty((n, c, d // 2, h // 2, w // 2), device=x.device, dtype=x.dtype)
+    idx = torch.empty((n, c, d // 2, h // 2, w // 2), device=x.device, dtype=torch.uint8)
+    desc = _pool_desc(x.shape, x.stride(), y.stride(), x.dtype)
+    rc = lib.r3c_maxpool2_fwd(ctypes.byref(desc), _ptr(x), _ptr(y), _ptr(idx), _stream_handle(x.device))
+    _check(lib, rc, "r3c_maxpool2_fwd")
+    return y, idx
+
+
+def maxpool2_bwd(dy: torch.Tensor, idx: torch.Tensor, x_shape) -> torch.Tensor:
+    """dx of MaxPool3d(2) (NCDHW, every element written)."""
+    lib = load()
+    dx = torch.empty(tuple(int(v) for v in x_shape), device=dy.device, dtype=dy.dtype)
+    desc = _pool_desc(dx.shape, dx.stride(), dy.stride(), dy.dtype)
+    rc = lib.r3c_maxpool2_bwd(ctypes.byref(desc), _ptr(dy), _ptr(idx), _ptr(dx), _stream_handle(dy.device))
+    _check(lib, rc, "r3c_maxpool2_bwd")
+    return dx

@@ -1,6 +1,5 @@
-"""Native BatchNorm3d + ReLU for the conv -> BatchNorm -> ReLU blocks of the
-UNet3D the reference accelerates (reference benches/unet_e2e.py:13-21,
-examples/drop_in_unet.py).
+"""Native BatchNorm3d + ReLU and MaxPool3d(2) for the UNet3D the reference
+accelerates (reference benches/unet_e2e.py:13-37, examples/drop_in_unet.py).
 
 BatchNormReLU3d is an opt-in replacement for the pair
 ``nn.BatchNorm3d(C), nn.ReLU(inplace=True)``: the same parameters, buffers
@@ -72,3 +71,47 @@ class BatchNormReLU3d(nn.BatchNorm3d):
         rv = self.running_var if track else None
         with torch.cuda.device(x.device):
             return _BnReluFn.apply(x, self.weight, self.bias, rm, rv, bn_training, float(factor), float(self.eps))
+
+
+class _MaxPool2Fn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        y, idx = _native.maxpool2_fwd(x)
+        ctx.save_for_backward(idx)
+        ctx.x_shape = tuple(x.shape)
+        ctx.mark_non_differentiable(idx)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (idx,) = ctx.saved_tensors
+        dy = dy.contiguous()
+        if dy.data_ptr() % 16:
+            dy = dy.clone()
+        return _native.maxpool2_bwd(dy, idx, ctx.x_shape)
+
+
+def _pair3(v):
+    return (v, v, v) if isinstance(v, int) else tuple(v)
+
+
+class MaxPool3dWmma(nn.MaxPool3d):
+    """nn.MaxPool3d; kernel 2, stride 2 (no padding, dilation, ceil_mode or
+    return_indices) runs the library's MaxPool3d kernels on CUDA NCDHW tensors
+    with even d, h and w a multiple of 8: PyTorch's maximum (first in window
+    order, NaN propagating), a one-byte window index kept for the backward
+    instead of a 64-bit one.  Anything else is nn.MaxPool3d."""
+
+    def _native_ok(self, x) -> bool:
+        stride = self.stride if self.stride is not None else self.kernel_size
+        return (_pair3(self.kernel_size) == (2, 2, 2) and _pair3(stride) == (2, 2, 2)
+                and _pair3(self.padding) == (0, 0, 0) and _pair3(self.dilation) == (1, 1, 1)
+                and not self.ceil_mode and not self.return_indices and x.is_cuda and _wmma_hw()
+                and x.numel() > 0 and _native.pool_ok(x))
+
+    def forward(self, x):
+        if not self._native_ok(x):
+            return super().forward(x)
+        _ensure_native(x.device)
+        with torch.cuda.device(x.device):
+            return _MaxPool2Fn.apply(x)

@@ -129,3 +129,15 @@ def test_bnrelu_on_cpu_is_batchnorm_then_relu():
     mod.eval()
     ref.eval()
     torch.testing.assert_close(mod(x), F.relu(ref(x)), atol=0, rtol=0)
+
+
+def test_maxpool_on_cpu_is_maxpool3d():
+    """MaxPool3dWmma is nn.MaxPool3d (same module type, state and output) off the
+    GPU and for every configuration other than kernel 2 / stride 2."""
+    from rdna4_conv3d.fused import MaxPool3dWmma
+    x = torch.randn(2, 3, 6, 8, 16, requires_grad=True)
+    for args in [(2,), (2, 2), (3, 1, 1), ((2, 2, 1),)]:
+        mod, ref = MaxPool3dWmma(*args), nn.MaxPool3d(*args)
+        assert isinstance(mod, nn.MaxPool3d)
+        assert not mod._native_ok(x)
+        torch.testing.assert_close(mod(x), ref(x), atol=0, rtol=0)

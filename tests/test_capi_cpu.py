@@ -51,6 +51,24 @@ def test_descriptor_layout_matches_c(tmp_path):
     assert [int(v) for v in got] == [ctypes.sizeof(D), D.kernel.offset, D.x_strides.offset, D.y_strides.offset]
 
 
+@pytest.mark.parametrize("name,fields", [
+    ("r3c_bn_desc", ("s", "y_strides", "g_strides", "o_strides", "training", "eps", "momentum")),
+    ("r3c_pool_desc", ("w", "x_strides", "y_strides")),
+])
+def test_bn_and_pool_descriptor_layouts_match_c(tmp_path, name, fields):
+    src = tmp_path / "layout.c"
+    offs = "".join(f", offsetof({name}, {f})" for f in fields)
+    fmt = " ".join(["%zu"] * (len(fields) + 1))
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "rdna4_conv3d.h"\n'
+        f'int main(void){{printf("{fmt}\\n", sizeof({name}){offs}); return 0;}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    D = _native.BnDesc if name == "r3c_bn_desc" else _native.PoolDesc
+    assert got == [ctypes.sizeof(D)] + [getattr(D, f).offset for f in fields]
+
+
 def _desc(k=3, pad=1, n=2, cin=8, cout=16, sp=(6, 7, 9), transpose=False, dtype=_native.R3C_BF16):
     import torch
     d, h, w = sp
@@ -170,3 +188,33 @@ def test_bn_workspace_query_validates_on_host():
     assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(0, 8, 16, _native.R3C_BF16))) == -1
     rc = lib.r3c_bn_relu_fwd(ctypes.byref(ok), None, None, None, None, None, None, None, None, None, 0, None)
     assert rc == _native.R3C_INVALID
+
+
+def test_pool_descriptors_validate_on_host():
+    """MaxPool3d(2) entry points reject shapes and strides the 16-byte kernels
+    do not take with R3C_UNSUPPORTED, and NULL pointers with R3C_INVALID, all
+    before any device call."""
+    lib = _native.load()
+
+    def call(shape, dtype=_native.R3C_BF16, xs=None, ys=None):
+        n, c, d, h, w = shape
+        desc = _native.PoolDesc()
+        desc.dtype, desc.n, desc.c, desc.d, desc.h, desc.w = dtype, n, c, d, h, w
+        pin = d * h * w
+        pout = pin // 8
+        desc.x_strides[0], desc.x_strides[1] = xs if xs else (c * pin, pin)
+        desc.y_strides[0], desc.y_strides[1] = ys if ys else (c * pout, pout)
+        return (lib.r3c_maxpool2_fwd(ctypes.byref(desc), None, None, None, None),
+                lib.r3c_maxpool2_bwd(ctypes.byref(desc), None, None, None, None))
+
+    U, I = _native.R3C_UNSUPPORTED, _native.R3C_INVALID
+    assert call((4, 24, 64, 128, 128)) == (I, I)          # valid descriptor, NULL pointers
+    assert call((2, 8, 4, 4, 8), _native.R3C_F32) == (I, I)
+    assert call((2, 8, 5, 4, 8)) == (U, U)                # odd d
+    assert call((2, 8, 4, 3, 8)) == (U, U)                # odd h
+    assert call((2, 8, 4, 4, 12)) == (U, U)               # w % 8
+    assert call((2, 8, 4, 4, 8), xs=(8 * 128 + 4, 128)) == (U, U)  # x sample stride not a multiple of 8
+    assert call((2, 8, 2, 2, 8)) == (I, I)                # y channel stride 4
+    assert call((2, 8, 4, 4, 8), ys=(8 * 16 + 2, 16)) == (U, U)    # y sample stride not a multiple of 4
+    assert call((2, 8, 4, 4, 8), dtype=7) == (U, U)
+    assert lib.r3c_maxpool2_fwd(None, None, None, None, None) == I

@@ -16,7 +16,8 @@ fp16 subnormals: MIOpen's dX flushes them (its error vs fp32 is about 1.0),
 the native dX keeps them (0.05-0.4), so there the native path must only be at
 least as accurate as stock.
 
-Over 40 steps (bf16): the loss curves of the native model and of stock must
+Over 40 steps (bf16): the loss curves of the native model (and of the model
+that also runs the native BatchNorm + ReLU and MaxPool3d(2)) and of stock must
 agree within 1e-2 -- a regression bound a wrong gradient exceeds within a few
 steps -- and the north star's own |dloss| <= 1e-3 is recorded as an expected
 failure: two correct bf16 computations of this model already differ by more
@@ -148,12 +149,14 @@ _CURVES = {}
 
 
 def _curves():
-    """40-step bf16 loss curves: native layers, stock, stock on the batch in reverse order."""
+    """40-step bf16 loss curves: native layers, native layers with the native
+    BatchNorm + ReLU and MaxPool3d(2), stock, stock on the batch in reverse order."""
     if _CURVES:
         return _CURVES
     import bench
     from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
     from rdna4_conv3d import _native as nat
+    from rdna4_conv3d.fused import BatchNormReLU3d, MaxPool3dWmma
 
     x, labels = _data()
     print("case unet3d 40 AMP bf16 steps: native", flush=True)
@@ -164,6 +167,14 @@ def _curves():
     kinds = {k for _, k, _ in nat.timing_collect()}
     nat.timing_enable(False)
     assert {"row", "wgrad"} <= kinds, kinds
+    print("case unet3d 40 AMP bf16 steps: native with BatchNormReLU3d and MaxPool3dWmma", flush=True)
+    nat.timing_enable(True)
+    nat.timing_collect()
+    _, all_native = bench.unet3d_train(Conv3dWmma, ConvTranspose3dWmma, 24, x, labels, STEPS - 3, 3,
+                                       bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma)
+    kinds = {k for _, k, _ in nat.timing_collect()}
+    nat.timing_enable(False)
+    assert {"row", "wgrad", "bn", "pool"} <= kinds, kinds
     print("case unet3d 40 AMP bf16 steps: stock", flush=True)
     _, stock = bench.unet3d_train(nn.Conv3d, nn.ConvTranspose3d, 24, x, labels, STEPS - 3, 3)
     print("case unet3d 40 AMP bf16 steps: stock, batch reversed", flush=True)
@@ -171,7 +182,7 @@ def _curves():
     _, stock_rev = bench.unet3d_train(nn.Conv3d, nn.ConvTranspose3d, 24, x[rev].contiguous(),
                                       labels[rev].contiguous(), STEPS - 3, 3)
     torch.cuda.empty_cache()
-    _CURVES.update(ours=ours, stock=stock, stock_rev=stock_rev)
+    _CURVES.update(ours=ours, all_native=all_native, stock=stock, stock_rev=stock_rev)
     return _CURVES
 
 
@@ -183,12 +194,15 @@ def _gap(a, b):
 @pytest.mark.timeout(1200)
 def test_unet3d_loss_tracks_stock():
     c = _curves()
-    assert len(c["ours"]) == len(c["stock"]) == STEPS
-    assert all(torch.isfinite(torch.tensor(c["ours"])))
+    assert len(c["ours"]) == len(c["all_native"]) == len(c["stock"]) == STEPS
+    assert all(torch.isfinite(torch.tensor(c["ours"] + c["all_native"])))
     g, ctrl = _gap(c["ours"], c["stock"]), _gap(c["stock_rev"], c["stock"])
-    print(f"  max |dloss| over {STEPS} steps: native vs stock {g:.3e}; stock vs stock batch-reversed {ctrl:.3e}; "
-          f"final {c['ours'][-1]:.5f} vs {c['stock'][-1]:.5f}", flush=True)
+    ga = _gap(c["all_native"], c["stock"])
+    print(f"  max |dloss| over {STEPS} steps: native vs stock {g:.3e}; all-native vs stock {ga:.3e}; "
+          f"stock vs stock batch-reversed {ctrl:.3e}; final {c['ours'][-1]:.5f} / {c['all_native'][-1]:.5f} vs "
+          f"{c['stock'][-1]:.5f}", flush=True)
     assert g <= REGRESSION_BOUND, f"native vs stock {g:.3e} > {REGRESSION_BOUND}"
+    assert ga <= REGRESSION_BOUND, f"all-native vs stock {ga:.3e} > {REGRESSION_BOUND}"
 
 
 @requires_gfx950
