@@ -180,6 +180,15 @@ constexpr int64_t kSplitTarget = 512;          // row-kernel jobs to aim for (tw
 constexpr int kNumCUs = 256;                   // MI355X compute units
 constexpr int64_t kMaxPartialBytes = 96ll << 20;
 
+// Row-walking k=3 weight gradient on (R3C_WGROW=0 turns it off).
+bool wgrow_enabled() {
+  static const bool v = [] {
+    const char* e = getenv("R3C_WGROW");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
@@ -811,7 +820,8 @@ struct WgPlan {
   int pw;              // 1: register-direct single-tap kernel (r3c_pwdw.h), fields below
   int tr, tc, nj;
   PwdwArgs pa;
-  int fl;  // 1: F staged channel-major from its w-contiguous source; 2: G too (k=1, no padding)
+  int fl;  // 1: F staged channel-major from its w-contiguous source; 2: G too (k=1, no padding);
+           // 3: k=3, G transposed from w-contiguous in the kernel; 5: k=3 row-walking kernel (r3c_wgrow.h)
   WgArgs a;
   size_t lds;
   int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
@@ -968,23 +978,40 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   // halved splits below, 96 loses 3.5 us and 192 gains 2).
   // The channel planes must be outermost in a sample: G's buffer range then
   // ends at channel Gc and the kernel gates no channel.
-  if (p.fl == 1 && p.mode == MODE_K3 && a.Gc <= 64 && a.gs[4] == 1 && a.Gw % 8 == 0 && a.gs[0] % 8 == 0 &&
-      a.gs[1] % 8 == 0 && a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0 && a.pw >= 0 && a.pw <= 6 && a.gs[2] > 0 &&
-      a.gs[3] > 0 && a.gs[1] >= (int64_t)(a.Gd - 1) * a.gs[2] + (int64_t)(a.Gh - 1) * a.gs[3] + a.Gw &&
-      2 * (int64_t)(a.Gc + 8) * a.gs[1] < (1ll << 30))  // no 32-bit wrap past the last channel group
-    p.fl = 3;
+  const bool g_wcontig =
+      p.fl == 1 && p.mode == MODE_K3 && a.gs[4] == 1 && a.Gw % 8 == 0 && a.gs[0] % 8 == 0 && a.gs[1] % 8 == 0 &&
+      a.gs[2] % 8 == 0 && a.gs[3] % 8 == 0 && a.pw >= 0 && a.pw <= 6 && a.gs[2] > 0 && a.gs[3] > 0 &&
+      a.gs[1] >= (int64_t)(a.Gd - 1) * a.gs[2] + (int64_t)(a.Gh - 1) * a.gs[3] + a.Gw &&
+      2 * (int64_t)(a.Gc + 8) * a.gs[1] < (1ll << 30);  // no 32-bit wrap past the last channel group
+  // k=3 with pad_w 1, the same w-contiguous sources 16-byte aligned (the
+  // caller's allow_copy) and rows of 64 or 128 positions: the row-walking
+  // kernel (fl 5, r3c_wgrow.h) fetches whole lines with no w halo, each x row
+  // once per column of output rows, and feeds the three kw taps of a (kd, kh)
+  // from one LDS read.
+  if (g_wcontig && allow_copy && a.pw == 1 && a.Rw == a.Gw && (a.Rw == 64 || a.Rw == 128) && wgrow_enabled())
+    p.fl = 5;
+  else if (g_wcontig && a.Gc <= 64) p.fl = 3;
   if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
     p.fcopy_bytes = align256(tensor_bytes(d->n, a.Fc, a.Rd, a.Rh, a.Rw));
     channels_last_strides(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
   }
-  if (copy_ok && p.fl != 3 && ncdhw_copyable(a.gs, a.Gc, a.Gd, a.Gh, a.Gw)) {
+  if (copy_ok && p.fl < 3 && ncdhw_copyable(a.gs, a.Gc, a.Gd, a.Gh, a.Gw)) {
     p.gcopy_bytes = align256(tensor_bytes(d->n, a.Gc, a.Gd, a.Gh, a.Gw));
     channels_last_strides(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   }
   a.f_bytes = sample_bytes(a.fs, a.Fc, a.Rd, a.Rh, a.Rw);
   a.g_bytes = p.fl == 3 ? (uint32_t)(2 * (int64_t)a.Gc * a.gs[1]) : sample_bytes(a.gs, a.Gc, a.Gd, a.Gh, a.Gw);
   // G channel range per tile: a multiple of 8 (16-byte staging) and of 4 (quads).
-  if (a.Gc <= 32) a.GCW = (a.Gc + 7) / 8 * 8;
+  if (p.fl == 5) {
+    // 8, 16 or 24 channels (9 GCW columns in blocks of 32, one block per
+    // wave): the width with the fewest column blocks over all G tiles.
+    int best = 0;
+    for (int gcw : {24, 16, 8}) {
+      const int64_t cost = cdiv(a.Gc, gcw) * cdiv(9 * gcw, 32);
+      if (!best || cost < cdiv(a.Gc, best) * cdiv(9 * best, 32)) best = gcw;
+    }
+    a.GCW = best;
+  } else if (a.Gc <= 32) a.GCW = (a.Gc + 7) / 8 * 8;
   else if (a.Gc % 32 == 0) a.GCW = 32;
   else if (a.Gc % 24 == 0) a.GCW = 24;
   else a.GCW = 32;
@@ -1002,12 +1029,29 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   else if (p.mode == MODE_K1) TD = WgGeom<MODE_K1>::TD, TH = WgGeom<MODE_K1>::TH, lds = WgGeom<MODE_K1>::LDS_BYTES;
   else TD = WgGeom<MODE_T2DW>::TD, TH = WgGeom<MODE_T2DW>::TH, lds = WgGeom<MODE_T2DW>::LDS_BYTES;
   if (p.fl == 3) lds += WgGeom<MODE_K3>::TRASH_BYTES;
+  if (p.fl == 5) {
+    if (a.Rw == 64)
+      lds = a.GCW == 8 ? WrGeom<8, 4>::LDS_BYTES : a.GCW == 16 ? WrGeom<16, 4>::LDS_BYTES : WrGeom<24, 4>::LDS_BYTES;
+    else
+      lds = a.GCW == 8 ? WrGeom<8, 8>::LDS_BYTES : a.GCW == 16 ? WrGeom<16, 8>::LDS_BYTES : WrGeom<24, 8>::LDS_BYTES;
+  }
   a.nbd = cdiv(a.Rd, TD);
   a.nbh = cdiv(a.Rh, TH);
   a.nbw = cdiv(a.Rw, 16);
-  const int64_t nbox = (int64_t)d->n * a.nbd * a.nbh * a.nbw;
-  a.nbox = (int32_t)std::min<int64_t>(nbox, (1ll << 31) - 1);
+  int64_t nbox = (int64_t)d->n * a.nbd * a.nbh * a.nbw;
   const int tiles = a.n_ftiles * a.n_gtiles;
+  if (p.fl == 5) {
+    // Jobs (n, d, h range): enough h ranges per (n, d) column to give every CU
+    // a workgroup, each range at least 8 rows long.
+    const int64_t cols = (int64_t)d->n * a.Rd;
+    int64_t hs = std::max<int64_t>(1, cdiv(kNumCUs, cols * tiles));
+    hs = std::min<int64_t>(hs, std::max(1, a.Rh / 8));
+    a.nbd = a.Rd;
+    a.nbh = (int32_t)hs;
+    a.nbw = 1;
+    nbox = cols * hs;
+  }
+  a.nbox = (int32_t)std::min<int64_t>(nbox, (1ll << 31) - 1);
   const int64_t per_split = (int64_t)a.Fpad * p.taps * a.Gpad * 4;
   // Enough workgroups to fill every CU at the LDS-limited occupancy, no more:
   // each extra split costs partial traffic.
@@ -1021,7 +1065,8 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   // is slower again, 133 and 79 us).
   const int64_t op_bytes =
       2 * (int64_t)d->n * ((int64_t)a.Fc * a.Rd * a.Rh * a.Rw + (int64_t)a.Gc * a.Gd * a.Gh * a.Gw);
-  if (nsplit * per_split > op_bytes) nsplit = std::max<int64_t>(1, nsplit / 2);
+  if (nsplit * per_split > op_bytes && p.fl != 5) nsplit = std::max<int64_t>(1, nsplit / 2);
+  if (p.fl == 5) nsplit = nbox;  // one job per workgroup, capped below
   nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, nbox));
   a.nsplit = (int32_t)nsplit;
@@ -1133,6 +1178,15 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   const bool g16b = (reinterpret_cast<uintptr_t>(a.gsrc) & 15) == 0;
   // fl 3 needs both sources 16-byte aligned; otherwise G falls back to scalar
   // staging (correct for any strides, slower).
+  if (p.fl == 5) {
+    // Planned only for 16-byte aligned sources (allow_copy).
+    if (!f16b || !g16b) return fail(R3C_INVALID, "internal: row-walking weight gradient planned for unaligned sources");
+    a.db_mode = db ? 1 : 0;
+    TimedLaunch tl(KIND_WGRAD, s);
+    const bool launched = launch_wgrow(d->dtype, a.GCW, a.Rw, a, s);
+    tl.end();
+    if (!launched) return fail(R3C_UNSUPPORTED, "no row-walking weight-gradient instantiation for %d channels", a.GCW);
+  } else {
   const int fl = (p.fl == 3 && f16b && g16b) ? 3 : (p.fl == 2 && f16b && g16b) ? 2 : ((p.fl && f16b) ? 1 : 0);
   const bool g_ok = vec16_ok(a.gsrc, a.gs) && a.Gc % 8 == 0;
   const int cl = fl == 3 ? 0 : fl == 2 ? 1 : ((g_ok && (fl || (vec16_ok(a.fsrc, a.fs) && a.Fc % 8 == 0))) ? 1 : 0);
@@ -1145,6 +1199,7 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   const bool launched = launch_wgrad(d->dtype, p.mode, p.cbw, cl, fl, a, p.lds, s);
   tl.end();
   if (!launched) return fail(R3C_UNSUPPORTED, "no weight-gradient instantiation for mode %d cbw %d", p.mode, p.cbw);
+  }
   rc = check_launch("weight-gradient kernel");
   if (rc) return rc;
   ReduceArgs r;
@@ -1279,6 +1334,10 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   WgPlan q;
   plan_wgrad(d, transpose, q, true);
   if (q.pw) need = std::max<int64_t>(need, wgrad_plan_ws(q));
+  // Unaligned sources take the plan without copies or the kw-shift kernel.
+  WgPlan u;
+  plan_wgrad(d, transpose, u, false, false);
+  if (!wgrad_plan_reject(u)) need = std::max<int64_t>(need, wgrad_plan_ws(u));
   return need;
 }
 

@@ -87,6 +87,29 @@ struct WgGeom {
   static constexpr int TRASH_BYTES = THREADS * 16;                    // k=3 NCDHW G staging: one slot per thread
 };
 
+// Geometry of the row-walking k=3 weight-gradient kernel (r3c_wgrow.h): rows
+// of W = 16 WL positions padded by 8 zero halves (pitch P); a step covers
+// RS = 16 / WL output rows (16 MFMA k-steps); x rows sit in a ring of
+// NSLOT = 2 RS + 2 slots of 3 x GCW rows, dY in two buffers of RS x 32 rows.
+template <int GCW, int WL>
+struct WrGeom {
+  static constexpr int W = 16 * WL, P = W + 8;
+  static constexpr int RS = 16 / WL;
+  static constexpr int NSLOT = 2 * RS + 2;
+  static constexpr int NCOL = 9 * GCW;
+  static constexpr int NTRIP = (NCOL + 31) / 32;
+  static constexpr int RING_HALVES = NSLOT * 3 * GCW * P;
+  static constexpr int FBUF_HALVES = RS * 32 * P;
+  static constexpr int THREADS = 512;
+  static constexpr int NFS = RS * 32 * (W / 8);        // dY staging items per step
+  static constexpr int NFI = (NFS + THREADS - 1) / THREADS;
+  static constexpr int NGS = RS * 3 * GCW * (W / 8);   // x staging items per step (RS rows of 3 planes)
+  static constexpr int NGI = (NGS + THREADS - 1) / THREADS;
+  static constexpr int LDS_BYTES = (RING_HALVES + 8 + 2 * FBUF_HALVES) * 2;
+  static_assert(NTRIP <= 7, "one wave per block and a free wave for the bias");
+  static_assert(16 % WL == 0, "rows per step");
+};
+
 struct WgArgs {
   const uint16_t* fsrc;  // F operand tensor (dY for Conv3d, x for ConvTranspose)
   const uint16_t* gsrc;  // G operand tensor (x for Conv3d, dY for ConvTranspose)
@@ -238,6 +261,8 @@ void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
 // One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
+// Row-walking k=3 weight gradient (r3c_wgrow.h); false if no instantiation for (gcw, W).
+bool launch_wgrow(int dtype, int gcw, int w, const WgArgs& a, hipStream_t stream);
 // Register-direct single-tap weight gradient (mode MODE_K1 with nj 4, or
 // MODE_T2DW with nj 1 / 2); false if no instantiation matches.
 bool launch_pwdw(int dtype, int mode, int tr, int tc, int nj, const PwdwArgs& a, hipStream_t stream);
