@@ -984,11 +984,12 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
       a.gs[1] >= (int64_t)(a.Gd - 1) * a.gs[2] + (int64_t)(a.Gh - 1) * a.gs[3] + a.Gw &&
       2 * (int64_t)(a.Gc + 8) * a.gs[1] < (1ll << 30);  // no 32-bit wrap past the last channel group
   // k=3 with pad_w 1, the same w-contiguous sources 16-byte aligned (the
-  // caller's allow_copy) and rows of 64 or 128 positions: the row-walking
+  // caller's allow_copy) and rows of 32, 64 or 128 positions: the row-walking
   // kernel (fl 5, r3c_wgrow.h) fetches whole lines with no w halo, each x row
   // once per column of output rows, and feeds the three kw taps of a (kd, kh)
   // from one LDS read.
-  if (g_wcontig && allow_copy && a.pw == 1 && a.Rw == a.Gw && (a.Rw == 64 || a.Rw == 128) && wgrow_enabled())
+  if (g_wcontig && allow_copy && a.pw == 1 && a.Rw == a.Gw &&
+      (a.Rw == 32 || a.Rw == 64 || a.Rw == 128) && wgrow_enabled())
     p.fl = 5;
   else if (g_wcontig && a.Gc <= 64) p.fl = 3;
   if (!p.fl && copy_ok && ncdhw_copyable(a.fs, a.Fc, a.Rd, a.Rh, a.Rw)) {
@@ -1030,10 +1031,10 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   else TD = WgGeom<MODE_T2DW>::TD, TH = WgGeom<MODE_T2DW>::TH, lds = WgGeom<MODE_T2DW>::LDS_BYTES;
   if (p.fl == 3) lds += WgGeom<MODE_K3>::TRASH_BYTES;
   if (p.fl == 5) {
-    if (a.Rw == 64)
-      lds = a.GCW == 8 ? WrGeom<8, 4>::LDS_BYTES : a.GCW == 16 ? WrGeom<16, 4>::LDS_BYTES : WrGeom<24, 4>::LDS_BYTES;
-    else
-      lds = a.GCW == 8 ? WrGeom<8, 8>::LDS_BYTES : a.GCW == 16 ? WrGeom<16, 8>::LDS_BYTES : WrGeom<24, 8>::LDS_BYTES;
+#define R3C_WR_LDS(WL_) (a.GCW == 8 ? WrGeom<8, WL_>::LDS_BYTES : a.GCW == 16 ? WrGeom<16, WL_>::LDS_BYTES \
+                                                               : WrGeom<24, WL_>::LDS_BYTES)
+    lds = a.Rw == 32 ? R3C_WR_LDS(2) : a.Rw == 64 ? R3C_WR_LDS(4) : R3C_WR_LDS(8);
+#undef R3C_WR_LDS
   }
   a.nbd = cdiv(a.Rd, TD);
   a.nbh = cdiv(a.Rh, TH);
@@ -1066,7 +1067,10 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   const int64_t op_bytes =
       2 * (int64_t)d->n * ((int64_t)a.Fc * a.Rd * a.Rh * a.Rw + (int64_t)a.Gc * a.Gd * a.Gh * a.Gw);
   if (nsplit * per_split > op_bytes && p.fl != 5) nsplit = std::max<int64_t>(1, nsplit / 2);
-  if (p.fl == 5) nsplit = nbox;  // one job per workgroup, capped below
+  // Row-walking jobs: one per workgroup while the partial sums stay below the
+  // operand bytes, else as many as fill every CU once (a workgroup then walks
+  // several columns).
+  if (p.fl == 5) nsplit = std::min<int64_t>(nbox, std::max<int64_t>(cdiv(kNumCUs, tiles), op_bytes / per_split));
   nsplit = std::min<int64_t>(nsplit, std::max<int64_t>(1, kMaxPartialBytes / per_split));
   nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, nbox));
   a.nsplit = (int32_t)nsplit;

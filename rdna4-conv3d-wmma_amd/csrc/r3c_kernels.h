@@ -89,12 +89,13 @@ struct WgGeom {
 
 // Geometry of the row-walking k=3 weight-gradient kernel (r3c_wgrow.h): rows
 // of W = 16 WL positions padded by 8 zero halves (pitch P); a step covers
-// RS = 16 / WL output rows (16 MFMA k-steps); x rows sit in a ring of
-// NSLOT = 2 RS + 2 slots of 3 x GCW rows, dY in two buffers of RS x 32 rows.
+// RS = min(16 / WL, 8) output rows (16 MFMA k-steps for W >= 32); x rows sit in a
+// ring of NSLOT = 2 RS + 2 slots of 3 x GCW rows, dY in two buffers of
+// RS x 32 rows.
 template <int GCW, int WL>
 struct WrGeom {
   static constexpr int W = 16 * WL, P = W + 8;
-  static constexpr int RS = 16 / WL;
+  static constexpr int RS = 16 / WL < 8 ? 16 / WL : 8;
   static constexpr int NSLOT = 2 * RS + 2;
   static constexpr int NCOL = 9 * GCW;
   static constexpr int NTRIP = (NCOL + 31) / 32;

@@ -1,5 +1,5 @@
 // r3c_wgrow.h -- k=3 Conv3d weight gradient that walks output rows, for
-// w-contiguous (NCDHW) operands with pad_w = 1 and W = 16 WL <= 128, on
+// w-contiguous (NCDHW) operands with pad_w = 1 and W = 32, 64 or 128, on
 // v_mfma_f32_32x32x16 (template body).
 //
 //   dW[f][g][kd][kh][kw] = sum over positions p of dY[p][f] * x[p + (kd, kh, kw) - pad][g]
@@ -11,7 +11,7 @@
 // (n, d, h, all W positions; WL MFMA k-steps of 16 positions), and a workgroup
 // walks a column of rows h0 .. h1-1 at fixed (n, d):
 //
-//   * a step covers RS = 16 / WL output rows (16 k-steps); the x rows they
+//   * a step covers RS = min(16 / WL, 8) output rows; the x rows they
 //     need are rows h - ph + kh (kh = 0..2) of the planes d - pd + kd, kept in
 //     a ring of 2 RS + 2 LDS slots, so each step stages RS new x rows per kd
 //     plane (whole 128-byte lines) and RS dY rows (32 channel rows);
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   constexpr int NT = Geo::THREADS, NSEG = W / 8;
   constexpr int NFI = Geo::NFI, NGI = Geo::NGI, NFS = Geo::NFS, NGS = Geo::NGS;
   constexpr int SLOT = 3 * GCW * P;  // halves per ring slot
-  constexpr int KSTEPS = RS * WL;    // MFMA k-steps per step (16)
+  constexpr int KSTEPS = RS * WL;    // MFMA k-steps per step (8 or 16)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;

@@ -17,9 +17,12 @@ bool launch_wl(int dtype, int gcw, const WgArgs& a, hipStream_t s) {
 }  // namespace
 
 bool launch_wgrow(int dtype, int gcw, int w, const WgArgs& a, hipStream_t s) {
-  if (w == 64) return launch_wl<4>(dtype, gcw, a, s);
-  if (w == 128) return launch_wl<8>(dtype, gcw, a, s);
-  return false;
+  switch (w) {
+    case 32: return launch_wl<2>(dtype, gcw, a, s);
+    case 64: return launch_wl<4>(dtype, gcw, a, s);
+    case 128: return launch_wl<8>(dtype, gcw, a, s);
+    default: return false;
+  }
 }
 
 }  // namespace r3c
