@@ -65,6 +65,11 @@ CONV_CASES = [
     (2, 24, 24, 16, 64, 64, 3, 1),   # more tiles than CUs: multi-job workgroups, no split K
     (2, 20, 24, 18, 70, 40, 3, 1),   # the same with ragged channels and box edges
     (2, 1, 24, 16, 64, 64, 3, 1),    # one source channel (the first UNet layer)
+    # NCDHW rows of 128 / 64 positions with enough boxes: full-width tap boxes
+    # (whole rows, 2 x 4 per box) with ragged d and h edges, and the
+    # row-walking dW over columns of odd length
+    (4, 8, 8, 13, 62, 128, 3, 1),
+    (4, 8, 16, 15, 30, 64, 3, 1),
     # k=1 unpadded with D*H*W % 64 == 0 (NCDHW: register-direct dW when Cout > 32):
     # 2 x 1 tile groups over two column groups, a 3 x 1 tile group
     (2, 96, 40, 4, 4, 32, 1, 0),
