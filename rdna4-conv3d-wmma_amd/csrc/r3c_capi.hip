@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <algorithm>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -741,8 +742,62 @@ bool t2dx_aligned(const void* dy, const void* dx) {
   return ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(dx)) & 3) == 0;
 }
 
+// k=1 without padding, at most 4 output channels, dense NCDHW planes of a
+// multiple of 8 positions: the streaming kernels of r3c_skinny.hip.
+bool skinny_ok(const r3c_conv_desc* d) {
+  if (d->kernel != 1 || d->pad_d || d->pad_h || d->pad_w || d->cout > 4 || d->cin > kSkinnyMaxC) return false;
+  const int64_t P = (int64_t)d->d * d->h * d->w;
+  if (P % 8 != 0 || (int64_t)d->n * (P / 8) >= (1ll << 31)) return false;
+  const int64_t* st[2] = {d->x_strides, d->y_strides};
+  for (const int64_t* t : st)
+    if (!(t[4] == 1 && t[3] == d->w && t[2] == (int64_t)d->h * d->w && t[1] % 8 == 0 && t[0] % 8 == 0 &&
+          t[1] >= P && t[0] > 0))
+      return false;
+  return true;
+}
+
+SkinnyArgs skinny_args(const r3c_conv_desc* d) {
+  SkinnyArgs a;
+  memset(&a, 0, sizeof a);
+  a.xs0 = d->x_strides[0];
+  a.xs1 = d->x_strides[1];
+  a.ys0 = d->y_strides[0];
+  a.ys1 = d->y_strides[1];
+  a.P = (int64_t)d->d * d->h * d->w;
+  a.ngroups = (int64_t)d->n * (a.P / 8);
+  a.C = d->cin;
+  a.O = d->cout;
+  return a;
+}
+
+bool aligned16_all(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (reinterpret_cast<uintptr_t>(p) & 15) return false;
+  return true;
+}
+
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
             int64_t ws_bytes, void* stream) {
+  if ((op == OP_CONV_FWD || op == OP_CONV_DX) && skinny_ok(d) && aligned16_all({src, dst}) && src && dst && w) {
+    int rc = check_device();
+    if (rc) return rc;
+    SkinnyArgs a = skinny_args(d);
+    a.w = static_cast<const uint16_t*>(w);
+    if (op == OP_CONV_FWD) {
+      a.x = const_cast<uint16_t*>(static_cast<const uint16_t*>(src));
+      a.y = static_cast<uint16_t*>(dst);
+      a.b = static_cast<const uint16_t*>(bias);
+    } else {
+      a.y = const_cast<uint16_t*>(static_cast<const uint16_t*>(src));
+      a.x = static_cast<uint16_t*>(dst);
+    }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    TimedLaunch tl(KIND_ROW, s);
+    const bool launched = launch_skinny(d->dtype, op == OP_CONV_FWD ? 0 : 1, a, s);
+    tl.end();
+    if (!launched) return fail(R3C_UNSUPPORTED, "no k=1 skinny instantiation for %d output channels", a.O);
+    return check_launch(op == OP_CONV_FWD ? "k=1 skinny forward" : "k=1 skinny dX");
+  }
   if (op == OP_T2_DX && t2dx_aligned(src, dst)) {
     T2dxPlan tp;
     if (plan_t2dx(d, tp)) return run_t2dx(d, tp, src, w, dst, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
@@ -1127,6 +1182,20 @@ int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void
 
 // Why a weight-gradient plan cannot run (nullptr: it can); shared with the
 // workspace query.
+// dW partials of the k=1 skinny kernel: one split per 1024 position groups, at most 1024.
+void plan_skinny_dw(const r3c_conv_desc* d, WgPlan& p) {
+  const SkinnyArgs s = skinny_args(d);
+  const int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(1024, s.ngroups / 1024));
+  p.a.nsplit = (int32_t)nsplit;
+  p.taps = 1;
+  p.part_bytes = align256(nsplit * (int64_t)s.O * s.C * 4);
+  p.dbpart_bytes = align256(nsplit * (int64_t)s.O * 4);
+  p.ngroups = cdiv(nsplit, kReduceGroup);
+  p.nelem = (int64_t)s.O * s.C + std::max(s.O, s.C);
+  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
+  p.fcopy_bytes = p.gcopy_bytes = 0;
+}
+
 const char* wgrad_plan_reject(const WgPlan& p) {
   if ((int64_t)p.lds > kMaxLds) return "the tile needs more LDS than a compute unit has";
   if (!p.pw && (p.a.f_bytes == 0 || p.a.g_bytes == 0))  // the register-direct plan checks its own
@@ -1143,6 +1212,56 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   // The register-direct single-tap kernel loads 16-byte vectors; other
   // alignments take the LDS-staged kernel, which stages any alignment.
   const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0;
+  if (!transpose && skinny_ok(d) && al16 && x && dy && dw && ws) {
+    WgPlan p;
+    plan_skinny_dw(d, p);
+    const int64_t need = wgrad_plan_ws(p);
+    if (ws_bytes < need)
+      return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
+    if (dw_dtype != R3C_F32 && dw_dtype != d->dtype) return fail(R3C_INVALID, "dw_dtype must be fp32 or the input dtype");
+    if (db && db_dtype != R3C_F32 && db_dtype != R3C_F16 && db_dtype != R3C_BF16)
+      return fail(R3C_INVALID, "db_dtype must be fp32, fp16 or bf16");
+    int rc = check_device();
+    if (rc) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    SkinnyArgs a = skinny_args(d);
+    a.x = const_cast<uint16_t*>(static_cast<const uint16_t*>(x));
+    a.y = const_cast<uint16_t*>(static_cast<const uint16_t*>(dy));
+    a.part = static_cast<float*>(ws);
+    a.dbpart = db ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes) : nullptr;
+    a.nsplit = p.a.nsplit;
+    {
+      TimedLaunch tl(KIND_WGRAD, s);
+      const bool launched = launch_skinny(d->dtype, 2, a, s);
+      tl.end();
+      if (!launched) return fail(R3C_UNSUPPORTED, "no k=1 skinny instantiation for %d output channels", a.O);
+    }
+    rc = check_launch("k=1 skinny dW");
+    if (rc) return rc;
+    ReduceArgs r;
+    memset(&r, 0, sizeof r);
+    r.part = a.part;
+    r.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
+    r.dw = dw;
+    r.db = db;
+    r.nsplit = a.nsplit;
+    r.Fc = a.O;
+    r.Gc = a.C;
+    r.taps = 1;
+    r.Fpad = a.O;
+    r.Gpad = a.C;
+    r.dw_dtype = dw_dtype;
+    r.db_dtype = db_dtype;
+    r.db_mode = db ? 1 : 0;
+    r.ngroups = p.ngroups;
+    r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
+    {
+      TimedLaunch tr(KIND_REDUCE, s);
+      launch_wgrad_reduce(r, s);
+      tr.end();
+    }
+    return check_launch("weight-gradient reduce");
+  }
   WgPlan p;
   plan_wgrad(d, transpose, p, al16, al16);  // unaligned: no copies either (same or less workspace)
   if (const char* why = wgrad_plan_reject(p)) return fail(R3C_UNSUPPORTED, "%s", why);
@@ -1338,6 +1457,11 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   WgPlan q;
   plan_wgrad(d, transpose, q, true);
   if (q.pw) need = std::max<int64_t>(need, wgrad_plan_ws(q));
+  if (!transpose && skinny_ok(d)) {
+    WgPlan k;
+    plan_skinny_dw(d, k);
+    need = std::max<int64_t>(need, wgrad_plan_ws(k));
+  }
   // Unaligned sources take the plan without copies or the kw-shift kernel.
   WgPlan u;
   plan_wgrad(d, transpose, u, false, false);

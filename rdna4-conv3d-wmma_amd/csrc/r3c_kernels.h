@@ -240,6 +240,21 @@ struct BnArgs {
 
 // MaxPool3d(2, stride 2) on NCDHW planes (r3c_pool.hip).  Even d, h, w with
 // w % 8 == 0: every input element belongs to exactly one window.
+// k=1 Conv3d with at most 4 output channels on dense NCDHW planes (r3c_skinny.hip).
+constexpr int kSkinnyMaxC = 64;  // input channels (weights staged in LDS)
+struct SkinnyArgs {
+  uint16_t* x;           // x (fwd, dW) or dx (dX): [n][C][P]
+  uint16_t* y;           // y (fwd) or dy (dX, dW): [n][O][P]
+  const uint16_t* w;     // [O][C]
+  const uint16_t* b;     // [O] or null (fwd)
+  float* part;           // dW: [nsplit][O][C] partial sums
+  float* dbpart;         // dW: [nsplit][O] or null
+  int64_t xs0, xs1, ys0, ys1;  // sample / channel strides (elements)
+  int64_t P;             // positions per plane (multiple of 8)
+  int64_t ngroups;       // n * P / 8
+  int32_t C, O, nsplit;
+};
+
 struct PoolArgs {
   const void* x;          // forward input
   void* y;                // forward output
@@ -275,6 +290,8 @@ void launch_t2dx_pack(const T2dxPackArgs& a, hipStream_t stream);
 void launch_bn_relu_fwd(int dtype, const BnArgs& a, hipStream_t stream);
 void launch_bn_relu_bwd(int dtype, const BnArgs& a, hipStream_t stream);
 // MaxPool3d(2): forward (y, idx) and backward (dx); dtype as the C ABI's codes.
+// pass 0 fwd, 1 dX, 2 dW partials; false if O is not 1..4.
+bool launch_skinny(int dtype, int pass, const SkinnyArgs& a, hipStream_t stream);
 void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);
 void launch_maxpool2_bwd(int dtype, const PoolArgs& a, hipStream_t stream);
 

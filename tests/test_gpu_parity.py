@@ -50,6 +50,11 @@ CONV_CASES = [
     # (n, cin, cout, d, h, w, k, pad)  -- the reference's test_conv3d.py:51-54 shapes first
     (2, 5, 7, 9, 11, 13, 3, 1),
     (2, 24, 1, 8, 16, 16, 1, 0),
+    # k=1 with at most 4 output channels on NCDHW: the streaming skinny kernels
+    # (the UNet3D head 24 -> 2; channel counts off the 8-channel blocks)
+    (2, 24, 2, 8, 16, 16, 1, 0),
+    (1, 40, 4, 4, 8, 24, 1, 0),
+    (3, 20, 3, 5, 6, 8, 1, 0),
     (1, 24, 24, 8, 16, 16, 3, 1),
     (1, 1, 24, 8, 16, 16, 3, 1),
     (1, 8, 16, 6, 7, 9, 3, 0),
