@@ -138,14 +138,16 @@ def _unet_block(cin, cout, conv, bnrelu=None):
     return nn.Sequential(conv(cin, cout, 3, padding=1), bnrelu(cout), conv(cout, cout, 3, padding=1), bnrelu(cout))
 
 
-def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None):
+def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None, cat_free=False):
     """UNet3D of BASELINE config 5: 4 levels (base, 2, 4, 8 x base channels),
     two (3x3x3 conv + BatchNorm + ReLU) per block, MaxPool3d(2) down,
     ConvTranspose3d k2s2 up with skip concat, 1x1x1 head to `classes`.
     `conv` / `tr` are the Conv3d / ConvTranspose3d classes to build with (the
     reference's factory pattern, benches/unet_e2e.py:13-32); `bnrelu`, if
     given, builds the fused BatchNorm + ReLU modules, `pool` the MaxPool3d(2)
-    module class (nn.MaxPool3d by default)."""
+    module class (nn.MaxPool3d by default); `cat_free` feeds each decoder
+    block's first conv the upsampled tensor and the skip tensor through its
+    forward_cat (no torch.cat) when the conv class has one."""
     import torch
     import torch.nn as nn
 
@@ -172,7 +174,11 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None):
                     skips.append(x)
                     x = self.pool(x)
             for up, dec, skip in zip(self.up, self.dec, reversed(skips)):
-                x = dec(torch.cat([up(x), skip], dim=1))
+                u = up(x)
+                if cat_free and hasattr(dec[0], "forward_cat"):
+                    x = dec[1:](dec[0].forward_cat(u, skip))
+                else:
+                    x = dec(torch.cat([u, skip], dim=1))
             return self.head(x)
 
     return UNet3D()
@@ -231,7 +237,7 @@ def _rounded_layers():
 
 
 def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False, bnrelu=None,
-                 pool=None):
+                 pool=None, cat_free=False):
     """AMP training of build_unet3d(conv, tr, base) on (x, labels):
     cross-entropy, Adam(lr=1e-3), autocast in `amp_dtype` (bf16 by default,
     BASELINE config 5; torch.float16 is the reference's protocol,
@@ -244,7 +250,7 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, chann
     import torch.nn as nn
     amp_dtype = amp_dtype or torch.bfloat16
     torch.manual_seed(1)
-    net = build_unet3d(conv, tr, base, bnrelu=bnrelu, pool=pool).to(x.device)
+    net = build_unet3d(conv, tr, base, bnrelu=bnrelu, pool=pool, cat_free=cat_free).to(x.device)
     if channels_last:
         net = net.to(memory_format=torch.channels_last_3d)
         x = x.contiguous(memory_format=torch.channels_last_3d)
@@ -354,8 +360,9 @@ def hbm_passes(layout: str, reps: int = 20):
 
 def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     """the UNet3D built with this package's layers (and, as
-    a second variant, with its fused BatchNorm + ReLU and MaxPool3d(2) as
-    well) against stock nn.Conv3d / nn.ConvTranspose3d, AMP bf16.
+    a second variant, with its fused BatchNorm + ReLU, MaxPool3d(2) and
+    concatenation-free decoder convs as well) against stock nn.Conv3d /
+    nn.ConvTranspose3d, AMP bf16.
 
     Loss tracking is reported against the spread of stock itself: the same
     stock model trained on the same batch with the sample order reversed (a
@@ -372,7 +379,7 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
     ms_f, loss_f = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup,
-                                bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma)
+                                bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma, cat_free=True)
     torch.cuda.empty_cache()
     ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup)
     torch.cuda.empty_cache()
@@ -393,7 +400,8 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
         "ms_per_sample": round(ms_w / batch, 3),
         "stock_ms_per_step": round(ms_s, 3),
         "speedup_vs_stock": round(ms_s / ms_w, 3),
-        "all_native_layers": "Conv3dWmma, ConvTranspose3dWmma, BatchNormReLU3d, MaxPool3dWmma",
+        "all_native_layers": "Conv3dWmma (decoder skip concatenation through forward_cat), ConvTranspose3dWmma, "
+                             "BatchNormReLU3d, MaxPool3dWmma",
         "all_native_ms_per_step": round(ms_f, 3),
         "all_native_ms_per_sample": round(ms_f / batch, 3),
         "all_native_speedup_vs_stock": round(ms_s / ms_f, 3),
@@ -410,8 +418,8 @@ def unet_probe(name: str) -> int:
     """Kernels of UNet3D training steps for a kernel trace (rocprofv3
     --kernel-trace --stats): `unet<base>[_fused|_stock]` runs 3 warmup + 5 AMP
     bf16 steps of BASELINE config 5 built with this package's layers (with its
-    BatchNorm + ReLU and MaxPool3d(2) as well for _fused, stock layers for
-    _stock)."""
+    BatchNorm + ReLU, MaxPool3d(2) and concatenation-free decoder convs as well
+    for _fused, stock layers for _stock)."""
     import torch
     import torch.nn as nn
     from rdna4_conv3d import Conv3dWmma, ConvTranspose3dWmma
@@ -426,7 +434,7 @@ def unet_probe(name: str) -> int:
     else:
         ms, _ = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, 5, 3,
                              bnrelu=BatchNormReLU3d if kind == "fused" else None,
-                             pool=MaxPool3dWmma if kind == "fused" else None)
+                             pool=MaxPool3dWmma if kind == "fused" else None, cat_free=kind == "fused")
     print(f"probe {name}: {ms:.3f} ms/step", flush=True)
     return 0
 

@@ -113,6 +113,37 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
                       void* dw, int32_t dw_dtype, void* db, int32_t db_dtype,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Conv3d over a channel concatenation ------------------------------------
+ * No counterpart in the reference package: it replaces the pair
+ * torch.cat((a, b), dim=1) + conv3d of the UNet3D decoder (the skip
+ * connection, benches/unet_e2e.py:38, examples/drop_in_unet.py:33) without
+ * writing the concatenated tensor.  `desc` describes the virtual x =
+ * cat(a, b): cin = channels of a + channels of b, x_strides those of a; `ca`
+ * is a's channel count (a positive multiple of 8 below cin), and b has the
+ * same channel / spatial strides with its own sample stride.  k = 3, NCDHW
+ * tensors whose (d, h, w) planes are dense, 16-byte aligned pointers; else
+ * R3C_UNSUPPORTED (and the workspace query returns -1): the caller then
+ * concatenates and calls r3c_conv3d_fwd / _dx / _dw.  The dX entry point
+ * writes the gradients of a and b into two tensors.  pass: 0 forward, 1 dX,
+ * 2 dW. */
+int64_t r3c_conv3d_cat_workspace(const r3c_conv_desc* desc, int32_t ca,
+                                 int64_t xb_sample_stride, int32_t pass);
+int32_t r3c_conv3d_cat_fwd(const r3c_conv_desc* desc, int32_t ca,
+                           const void* xa, const void* xb,
+                           int64_t xb_sample_stride, const void* w,
+                           const void* bias, void* y, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+int32_t r3c_conv3d_cat_dx(const r3c_conv_desc* desc, int32_t ca,
+                          const void* dy, const void* w, void* dxa, void* dxb,
+                          int64_t xb_sample_stride, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+int32_t r3c_conv3d_cat_dw(const r3c_conv_desc* desc, int32_t ca,
+                          const void* xa, const void* xb,
+                          int64_t xb_sample_stride, const void* dy, void* dw,
+                          int32_t dw_dtype, void* db, int32_t db_dtype,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 /* ---- Conv3d dW without a caller workspace -------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -776,9 +776,35 @@ bool aligned16_all(std::initializer_list<const void*> ps) {
   return true;
 }
 
+// Descriptor checks of a channel concatenation (see CatSpec): k=3, NCDHW
+// planes dense in (d, h, w), the split a positive multiple of 8 below cin, and
+// sample strides that hold each tensor's channel planes.
+int cat_check(const r3c_conv_desc* d, int32_t ca, int64_t xb_s0) {
+  int rc = validate(d, false);
+  if (rc) return rc;
+  const int64_t* st = d->x_strides;
+  if (d->kernel != 3) return fail(R3C_UNSUPPORTED, "channel concatenation: kernel must be 3");
+  if (ca <= 0 || ca >= d->cin || ca % 8) return fail(R3C_UNSUPPORTED, "channel concatenation: split %d", ca);
+  if (!(st[4] == 1 && st[3] == d->w && st[2] == (int64_t)d->h * d->w && st[1] % 8 == 0 && st[0] % 8 == 0 &&
+        st[1] >= (int64_t)d->d * d->h * d->w && st[0] >= (int64_t)ca * st[1] && xb_s0 % 8 == 0 &&
+        xb_s0 >= (int64_t)(d->cin - ca) * st[1]))
+    return fail(R3C_UNSUPPORTED, "channel concatenation: tensors must be NCDHW with dense (d, h, w) planes");
+  return R3C_OK;
+}
+
+// Channel concatenation [A, B] as the x of a k=3 Conv3d (the r3c_conv3d_cat_*
+// entry points): A has `ca` channels and the descriptor's x strides, B the
+// same channel and spatial strides and its own sample stride.
+struct CatSpec {
+  int32_t ca;
+  const void* xb;   // forward and dW: B
+  void* dxb;        // dX: B's gradient
+  int64_t xb_s0;
+};
+
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
-            int64_t ws_bytes, void* stream) {
-  if ((op == OP_CONV_FWD || op == OP_CONV_DX) && skinny_ok(d) && aligned16_all({src, dst}) && src && dst && w) {
+            int64_t ws_bytes, void* stream, const CatSpec* cat = nullptr) {
+  if (!cat && (op == OP_CONV_FWD || op == OP_CONV_DX) && skinny_ok(d) && aligned16_all({src, dst}) && src && dst && w) {
     int rc = check_device();
     if (rc) return rc;
     SkinnyArgs a = skinny_args(d);
@@ -805,6 +831,14 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   RowPlan p;
   plan_row(d, op, p);
   if (p.copy_bytes && (reinterpret_cast<uintptr_t>(src) & 15)) plan_row(d, op, p, false);  // same or less workspace
+  if (cat) {
+    // The concatenation is read by the w-contiguous staging (forward) or
+    // written by the NCDHW epilogue (dX) of the tap kernel, from 16-byte
+    // aligned tensors; anything else has no plan here.
+    if (!p.tap || p.copy_bytes || (op == OP_CONV_FWD && p.cl != 3) ||
+        !aligned16_all({src, dst, op == OP_CONV_FWD ? cat->xb : static_cast<const void*>(cat->dxb)}))
+      return fail(R3C_UNSUPPORTED, "no plan for this channel concatenation");
+  }
   if (const char* why = row_plan_reject(p)) return fail(R3C_UNSUPPORTED, "%s", why);
   const int64_t need = row_plan_ws(p);
   if (ws_bytes < need)
@@ -836,6 +870,19 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
   a.wpk = static_cast<const uint16_t*>(ws);
   a.bias = static_cast<const uint16_t*>(bias);
   a.dst = static_cast<uint16_t*>(dst);
+  if (cat && op == OP_CONV_FWD) {
+    a.src2 = static_cast<const uint16_t*>(cat->xb);
+    a.ss0_2 = cat->xb_s0;
+    a.csplit = cat->ca;
+    a.src_bytes = (uint32_t)(2 * (int64_t)cat->ca * a.ss[1]);
+    a.src2_bytes = (uint32_t)(2 * (int64_t)(d->cin - cat->ca) * a.ss[1]);
+  } else if (cat) {
+    a.dst2 = static_cast<uint16_t*>(cat->dxb);
+    a.sd0_2 = cat->xb_s0;
+    a.dsplit = cat->ca;
+    a.dst_bytes = (uint32_t)(2 * (int64_t)cat->ca * a.sd[1]);
+    a.dst2_bytes = (uint32_t)(2 * (int64_t)(d->cin - cat->ca) * a.sd[1]);
+  }
   // 16-byte staging needs a 16-byte aligned source; otherwise stage by scalars.
   const int cl = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? p.cl : 0;
   a.src_cl = cl;
@@ -970,7 +1017,9 @@ bool plan_pwdw(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
 
 // allow_pw false: no register-direct plan (it needs 16-byte aligned sources);
 // allow_copy false: no NDHWC copy of an operand (likewise).
-void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw = true, bool allow_copy = true) {
+// gcw_div > 0: G tiles must not straddle channel gcw_div (a channel concatenation's split).
+void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw = true, bool allow_copy = true,
+                int gcw_div = 0) {
   WgArgs& a = p.a;
   memset(&a, 0, sizeof a);
   if (transpose) {
@@ -1063,6 +1112,7 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
     // wave): the width with the fewest column blocks over all G tiles.
     int best = 0;
     for (int gcw : {24, 16, 8}) {
+      if (gcw_div > 0 && gcw_div % gcw != 0) continue;
       const int64_t cost = cdiv(a.Gc, gcw) * cdiv(9 * gcw, 32);
       if (!best || cost < cdiv(a.Gc, best) * cdiv(9 * best, 32)) best = gcw;
     }
@@ -1208,11 +1258,11 @@ int64_t wgrad_plan_ws(const WgPlan& p) {
 }
 
 int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void* dy, void* dw, int dw_dtype, void* db,
-              int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
+              int db_dtype, void* ws, int64_t ws_bytes, void* stream, const CatSpec* cat = nullptr) {
   // The register-direct single-tap kernel loads 16-byte vectors; other
   // alignments take the LDS-staged kernel, which stages any alignment.
   const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0;
-  if (!transpose && skinny_ok(d) && al16 && x && dy && dw && ws) {
+  if (!cat && !transpose && skinny_ok(d) && al16 && x && dy && dw && ws) {
     WgPlan p;
     plan_skinny_dw(d, p);
     const int64_t need = wgrad_plan_ws(p);
@@ -1263,7 +1313,9 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
     return check_launch("weight-gradient reduce");
   }
   WgPlan p;
-  plan_wgrad(d, transpose, p, al16, al16);  // unaligned: no copies either (same or less workspace)
+  plan_wgrad(d, transpose, p, al16, al16, cat ? cat->ca : 0);  // unaligned: no copies either (same or less workspace)
+  if (cat && (p.fl != 5 || !aligned16_all({x, dy, cat->xb})))
+    return fail(R3C_UNSUPPORTED, "no weight-gradient plan for this channel concatenation");
   if (const char* why = wgrad_plan_reject(p)) return fail(R3C_UNSUPPORTED, "%s", why);
   const int64_t need = wgrad_plan_ws(p);
   if (ws_bytes < need)
@@ -1279,6 +1331,13 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   WgArgs a = p.a;
   a.fsrc = static_cast<const uint16_t*>(transpose ? x : dy);
   a.gsrc = static_cast<const uint16_t*>(transpose ? dy : x);
+  if (cat) {
+    a.gsrc2 = static_cast<const uint16_t*>(cat->xb);
+    a.gs0_2 = cat->xb_s0;
+    a.gsplit = cat->ca;
+    a.g_bytes = (uint32_t)(2 * (int64_t)cat->ca * a.gs[1]);
+    a.g2_bytes = (uint32_t)(2 * (int64_t)(d->cin - cat->ca) * a.gs[1]);
+  }
   {
     char* copies = static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
     if (p.fcopy_bytes) {
@@ -1552,6 +1611,52 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* d, const void* x, const void* dy, voi
   int rc = validate(d, false);
   if (rc) return rc;
   return run_wgrad(d, false, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
+}
+
+int64_t r3c_conv3d_cat_workspace(const r3c_conv_desc* d, int32_t ca, int64_t xb_sample_stride, int32_t pass) {
+  if (cat_check(d, ca, xb_sample_stride) != R3C_OK) return -1;
+  if (pass == 0 || pass == 1) {
+    RowPlan p;
+    plan_row(d, pass == 0 ? OP_CONV_FWD : OP_CONV_DX, p);
+    if (row_plan_reject(p) || !p.tap || p.copy_bytes || (pass == 0 && p.cl != 3)) return -1;
+    return row_plan_ws(p);
+  }
+  if (pass == 2) {
+    WgPlan p;
+    plan_wgrad(d, false, p, true, true, ca);
+    if (wgrad_plan_reject(p) || p.fl != 5) return -1;
+    return wgrad_plan_ws(p);
+  }
+  return -1;
+}
+
+int32_t r3c_conv3d_cat_fwd(const r3c_conv_desc* d, int32_t ca, const void* xa, const void* xb,
+                           int64_t xb_sample_stride, const void* w, const void* bias, void* y, void* ws,
+                           int64_t ws_bytes, void* stream) {
+  int rc = cat_check(d, ca, xb_sample_stride);
+  if (rc) return rc;
+  if (!xb) return fail(R3C_INVALID, "NULL tensor pointer");
+  const CatSpec cs{ca, xb, nullptr, xb_sample_stride};
+  return run_row(d, OP_CONV_FWD, xa, w, bias, y, ws, ws_bytes, stream, &cs);
+}
+
+int32_t r3c_conv3d_cat_dx(const r3c_conv_desc* d, int32_t ca, const void* dy, const void* w, void* dxa, void* dxb,
+                          int64_t xb_sample_stride, void* ws, int64_t ws_bytes, void* stream) {
+  int rc = cat_check(d, ca, xb_sample_stride);
+  if (rc) return rc;
+  if (!dxb) return fail(R3C_INVALID, "NULL tensor pointer");
+  const CatSpec cs{ca, nullptr, dxb, xb_sample_stride};
+  return run_row(d, OP_CONV_DX, dy, w, nullptr, dxa, ws, ws_bytes, stream, &cs);
+}
+
+int32_t r3c_conv3d_cat_dw(const r3c_conv_desc* d, int32_t ca, const void* xa, const void* xb,
+                          int64_t xb_sample_stride, const void* dy, void* dw, int32_t dw_dtype, void* db,
+                          int32_t db_dtype, void* ws, int64_t ws_bytes, void* stream) {
+  int rc = cat_check(d, ca, xb_sample_stride);
+  if (rc) return rc;
+  if (!xb) return fail(R3C_INVALID, "NULL tensor pointer");
+  const CatSpec cs{ca, xb, nullptr, xb_sample_stride};
+  return run_wgrad(d, false, xa, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream, &cs);
 }
 
 int64_t r3c_bn_relu_workspace(const r3c_bn_desc* d) {

@@ -57,6 +57,15 @@ struct RowArgs {
   int32_t phase;           // 0: main pass; 1: split-K epilogue pass, one workgroup per tile
   int32_t chan_outer;      // 1: src_bytes ends at channel Cs (channel planes outermost in a sample),
                            //    so loads of channels past Cs fall out of range by themselves
+  // A channel concatenation [A, B] without a copy (k=3 tap kernel, NCDHW): source
+  // channels >= csplit are channels - csplit of src2, destination channels
+  // >= dsplit go to dst2 (0: one tensor).  Channel and spatial strides are
+  // those of ss / sd; src2 / dst2 have their own sample stride and range.
+  const uint16_t* src2;
+  uint16_t* dst2;
+  int64_t ss0_2, sd0_2;
+  uint32_t src2_bytes, dst2_bytes;
+  int32_t csplit, dsplit;
 };
 
 // Weight-gradient box geometry, fixed per mode: TD x TH lines of 16
@@ -129,6 +138,13 @@ struct WgArgs {
   int32_t Fpad, Gpad;
   int32_t db_mode;         // 0 none, 1 db = sum over F, 2 db = sum over G
   int32_t nblocks;
+  // G over a channel concatenation [A, B] (row-walking kernel): G channels
+  // >= gsplit are channels - gsplit of gsrc2 (0: one tensor); G tiles do not
+  // straddle gsplit.
+  const uint16_t* gsrc2;
+  int64_t gs0_2;
+  uint32_t g2_bytes;
+  int32_t gsplit;
 };
 
 // Register-direct weight gradient of the single-tap passes (Conv3d k=1

@@ -147,7 +147,11 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
   const int g = lane >> 5, li = lane & 31;
   const int r0d = ec.bd * TD, r0h = ec.bh * TH * HR, r0w = ec.bw * LW;
   const int64_t* sd = a.sd;
-  const __amdgpu_buffer_rsrc_t dst = make_rsrc(a.dst + (int64_t)ec.n * sd[0], a.dst_bytes);
+  const __amdgpu_buffer_rsrc_t dst1 = make_rsrc(a.dst + (int64_t)ec.n * sd[0], a.dst_bytes);
+  // Destination channels >= dsplit (a multiple of 8) go to the second tensor
+  // of a channel concatenation.
+  const __amdgpu_buffer_rsrc_t dst2 =
+      a.dsplit > 0 ? make_rsrc(a.dst2 + (int64_t)ec.n * a.sd0_2, a.dst2_bytes) : dst1;
   const bool pos_contig = sd[4] == 1;
   const bool ch_contig = !pos_contig && sd[1] == 1;
   const int sd1 = (int)sd[1], sd2 = (int)sd[2], sd3 = (int)sd[3], sd4 = (int)sd[4];
@@ -172,8 +176,11 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
       const float4* bt = reinterpret_cast<const float4*>(btab + (colbase - bcol0)) + g;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int c0 = colbase + 8 * q + 4 * g;  // channels c0 .. c0+3 of this lane
         if (colbase + 8 * q >= a.ncols) break;   // uniform: the rest of the block is padding
+        const bool second = a.dsplit > 0 && colbase + 8 * q >= a.dsplit;  // uniform
+        const __amdgpu_buffer_rsrc_t dst = second ? dst2 : dst1;
+        const int cbase = second ? a.dsplit : 0;
+        const int c0 = colbase + 8 * q + 4 * g - cbase;  // channels c0 .. c0+3 of this lane (in dst)
         const float4 bv = bt[2 * q];
         const float v0 = acc[mb][nb][4 * q + 0] + bv.x, v1 = acc[mb][nb][4 * q + 1] + bv.y;
         const float v2 = acc[mb][nb][4 * q + 2] + bv.z, v3 = acc[mb][nb][4 * q + 3] + bv.w;
@@ -189,20 +196,20 @@ __device__ __forceinline__ void tap_epilogue(const RowArgs& a, f32x16_t (&acc)[M
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
               const uint32_t off = poff + 2u * (uint32_t)((c0 + rr) * sd1);
-              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off, pos_ok && c0 + rr < a.ncols), 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off, pos_ok && cbase + c0 + rr < a.ncols), 0, 0);
             }
           }
         } else {
           typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
           const uint32_t off = poff + 2u * (uint32_t)c0;
-          if (c0 + 4 <= a.ncols) {
+          if (cbase + c0 + 4 <= a.ncols) {
             const u32x2_t v = {pack2(from_f32<T>(v0), from_f32<T>(v1)), pack2(from_f32<T>(v2), from_f32<T>(v3))};
             __builtin_amdgcn_raw_buffer_store_b64(v, dst, clean ? (int)off : gate(off, pos_ok), 0, 0);
           } else {
             const float vv[4] = {v0, v1, v2, v3};
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr)
-              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off + 2u * rr, pos_ok && c0 + rr < a.ncols),
+              __builtin_amdgcn_raw_buffer_store_b16(from_f32<T>(vv[rr]), dst, gate(off + 2u * rr, pos_ok && cbase + c0 + rr < a.ncols),
                                                     0, 0);
           }
         }
@@ -363,13 +370,18 @@ __global__ __launch_bounds__(512) void tap_kernel(const RowArgs a) {
       // The host takes this mode only with channel planes outermost in a
       // sample and the buffer range ending at channel Cs, so loads of channels
       // past Cs fall out of range by themselves; a stage past the end gets an
-      // empty range.  No per-load gating.
-      const __amdgpu_buffer_rsrc_t src =
-          make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), live ? a.src_bytes : 0u);
+      // empty range.  No per-load gating.  A chunk at or past csplit (a
+      // multiple of 8) comes from the concatenation's second tensor.
+      const bool second = a.csplit > 0 && c0 >= a.csplit;  // uniform
+      const uint16_t* sbase = second ? a.src2 : a.src;
+      const int64_t s0 = second ? a.ss0_2 : a.ss[0];
+      const uint32_t srange = second ? a.src2_bytes : a.src_bytes;
+      const uint32_t coff2 = second ? 2u * (uint32_t)(c0 - a.csplit) * ss1 : coff;
+      const __amdgpu_buffer_rsrc_t src = make_rsrc(sbase + (live ? (int64_t)cur.n * s0 : 0), live ? srange : 0u);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         pfa[slot][e] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)(soff[0] + coff + 2u * e * ss1), 0, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)(soff[0] + coff2 + 2u * e * ss1), 0, 0));
     } else {
       const __amdgpu_buffer_rsrc_t src = make_rsrc(a.src + (live ? (int64_t)cur.n * a.ss[0] : 0), a.src_bytes);
 #pragma unroll

@@ -86,6 +86,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   uint16_t* const fbuf = lds + RING + 8;  // after the ring's trailing zero slot
   const int fc0 = ft * 32;
   const int gc0 = gt * GCW;
+  // G of a channel concatenation: the tile's channels lie in one tensor.
+  const bool gsec = a.gsplit > 0 && gc0 >= a.gsplit;  // uniform
+  const uint16_t* const gptr = gsec ? a.gsrc2 : a.gsrc;
+  const int64_t gsamp = gsec ? a.gs0_2 : a.gs[0];
+  const uint32_t grange = gsec ? a.g2_bytes : a.g_bytes;
+  const int gcl = gsec ? gc0 - a.gsplit : gc0;  // the tile's first channel in its tensor
 
   // Zero slots: the 8 leading halves of every ring row, and one after the ring
   // (dY rows are never read outside their W positions).
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const bool ex = it < NGS;
     grow[k] = ex ? r : -1;
     gkd[k] = pk;
-    grel[k] = 2 * ((gc0 + ch) * gs1 + 8 * seg);
+    grel[k] = 2 * ((gcl + ch) * gs1 + 8 * seg);
     gval[k] = ex && gc0 + ch < a.Gc;
     gslot[k] = (pk * GCW + ch) * P + 8 + 8 * seg;  // plus the ring slot of row r
   }
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   // d - pd + kd); rows outside [0, Gh) read as zero.
   auto issue = [&](int n, int d, int hf, int nf, int xr, int nx) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t fsrc = make_rsrc_u(a.fsrc + (int64_t)n * a.fs[0], a.f_bytes);
-    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc_u(a.gsrc + (int64_t)n * a.gs[0], a.g_bytes);
+    const __amdgpu_buffer_rsrc_t gsrc = make_rsrc_u(gptr + (int64_t)n * gsamp, grange);
     const int fbase = 2 * (d * fs2 + hf * fs3);
 #pragma unroll
     for (int k = 0; k < NFI; ++k) {

@@ -118,6 +118,14 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_bn_relu_fwd.argtypes = [B, P, P, P, P, P, P, P, P, P, I64, P]
     lib.r3c_bn_relu_bwd.restype = I32
     lib.r3c_bn_relu_bwd.argtypes = [B, P, P, P, P, P, P, P, P, P, P, I64, P]
+    lib.r3c_conv3d_cat_workspace.restype = ctypes.c_int64
+    lib.r3c_conv3d_cat_workspace.argtypes = [D, I32, ctypes.c_int64, I32]
+    lib.r3c_conv3d_cat_fwd.restype = I32
+    lib.r3c_conv3d_cat_fwd.argtypes = [D, I32, P, P, ctypes.c_int64, P, P, P, P, ctypes.c_int64, P]
+    lib.r3c_conv3d_cat_dx.restype = I32
+    lib.r3c_conv3d_cat_dx.argtypes = [D, I32, P, P, P, P, ctypes.c_int64, P, ctypes.c_int64, P]
+    lib.r3c_conv3d_cat_dw.restype = I32
+    lib.r3c_conv3d_cat_dw.argtypes = [D, I32, P, P, ctypes.c_int64, P, P, I32, P, I32, P, ctypes.c_int64, P]
     Q = ctypes.POINTER(PoolDesc)
     lib.r3c_maxpool2_fwd.restype = I32
     lib.r3c_maxpool2_fwd.argtypes = [Q, P, P, P, P]
@@ -541,3 +549,96 @@ def maxpool2_bwd(dy: torch.Tensor, idx: torch.Tensor, x_shape) -> torch.Tensor:
     rc = lib.r3c_maxpool2_bwd(ctypes.byref(desc), _ptr(dy), _ptr(idx), _ptr(dx), _stream_handle(dy.device))
     _check(lib, rc, "r3c_maxpool2_bwd")
     return dx
+
+
+# ---------------------------------------------------------------------------
+# Conv3d over a channel concatenation [a, b] (no torch.cat)
+# ---------------------------------------------------------------------------
+def cat_tensors_ok(xa: torch.Tensor, xb: torch.Tensor) -> bool:
+    """Pairs the concatenation entry points take: contiguous NCDHW, same
+    dtype, device and (n, d, h, w), a's channels a multiple of 8, 16-byte
+    aligned."""
+    if xa.dim() != 5 or xb.dim() != 5 or xa.dtype != xb.dtype or xa.device != xb.device:
+        return False
+    if xa.shape[0] != xb.shape[0] or xa.shape[2:] != xb.shape[2:] or int(xa.shape[1]) % 8:
+        return False
+    return (xa.is_contiguous() and xb.is_contiguous() and xa.data_ptr() % 16 == 0 and xb.data_ptr() % 16 == 0
+            and xa.numel() > 0 and xb.numel() > 0)
+
+
+def _cat_desc(xa_shape, cb: int, y_shape, k: int, padding, dtype, y_strides) -> ConvDesc:
+    n, ca, d, h, w = (int(v) for v in xa_shape)
+    x_shape = (n, ca + int(cb), d, h, w)
+    xs = _dense_strides((n, ca, d, h, w), False)
+    return make_desc(x_shape, y_shape, k, padding, dtype, xs, y_strides)
+
+
+@lru_cache(maxsize=1024)
+def _cat_plans_ok(xa_shape, cb: int, y_shape, padding, dtype_code: int) -> bool:
+    lib = load()
+    d = _cat_desc(xa_shape, cb, y_shape, 3, padding, torch.bfloat16, _dense_strides(y_shape, False))
+    d.dtype = dtype_code
+    xb_s0 = int(cb) * int(xa_shape[2]) * int(xa_shape[3]) * int(xa_shape[4])
+    return all(lib.r3c_conv3d_cat_workspace(ctypes.byref(d), int(xa_shape[1]), xb_s0, p) >= 0 for p in (0, 1, 2))
+
+
+def cat_plans_ok(xa: torch.Tensor, xb: torch.Tensor, weight_shape, padding, dtype: torch.dtype) -> bool:
+    """True when all three passes of a k=3 Conv3d over cat(xa, xb) have plans."""
+    n, ca, d, h, w = (int(v) for v in xa.shape)
+    pd = tuple(int(v) for v in padding)
+    y_shape = (n, int(weight_shape[0]), d + 2 * pd[0] - 2, h + 2 * pd[1] - 2, w + 2 * pd[2] - 2)
+    return _cat_plans_ok(tuple(int(v) for v in xa.shape), int(xb.shape[1]), y_shape, pd, _DTYPE_CODE[dtype])
+
+
+def conv3d_cat_fwd(xa, xb, weight, bias, padding):
+    """conv3d(cat((xa, xb), 1), weight) + bias, k = 3, without the concatenation."""
+    lib = load()
+    weight = weight.contiguous()
+    n, ca, d, h, w = _dims5(xa)
+    cout = int(weight.shape[0])
+    y = torch.empty((n, cout, d + 2 * padding[0] - 2, h + 2 * padding[1] - 2, w + 2 * padding[2] - 2),
+                    device=xa.device, dtype=xa.dtype)
+    desc = _cat_desc(xa.shape, xb.shape[1], y.shape, 3, padding, xa.dtype, y.stride())
+    xb_s0 = int(xb.stride(0))
+    ws = _workspace(lib.r3c_conv3d_cat_workspace(ctypes.byref(desc), ca, xb_s0, 0), xa.device, "r3c_conv3d_cat_fwd")
+    b = bias.contiguous() if bias is not None else None
+    rc = lib.r3c_conv3d_cat_fwd(ctypes.byref(desc), ca, _ptr(xa), _ptr(xb), xb_s0, _ptr(weight), _ptr(b), _ptr(y),
+                                _ptr(ws), ws.numel(), _stream_handle(xa.device))
+    _check(lib, rc, "r3c_conv3d_cat_fwd")
+    return y
+
+
+def conv3d_cat_dx(go, weight, xa_shape, xb_shape, padding):
+    """(dxa, dxb): the dX of a k=3 Conv3d over cat(xa, xb), split by channels."""
+    lib = load()
+    go = go.contiguous()
+    weight = weight.contiguous()
+    dxa = torch.empty(tuple(int(v) for v in xa_shape), device=go.device, dtype=go.dtype)
+    dxb = torch.empty(tuple(int(v) for v in xb_shape), device=go.device, dtype=go.dtype)
+    ca = int(xa_shape[1])
+    desc = _cat_desc(xa_shape, xb_shape[1], go.shape, 3, padding, go.dtype, go.stride())
+    xb_s0 = int(dxb.stride(0))
+    ws = _workspace(lib.r3c_conv3d_cat_workspace(ctypes.byref(desc), ca, xb_s0, 1), go.device, "r3c_conv3d_cat_dx")
+    rc = lib.r3c_conv3d_cat_dx(ctypes.byref(desc), ca, _ptr(go), _ptr(weight), _ptr(dxa), _ptr(dxb), xb_s0, _ptr(ws),
+                               ws.numel(), _stream_handle(go.device))
+    _check(lib, rc, "r3c_conv3d_cat_dx")
+    return dxa, dxb
+
+
+def conv3d_cat_dw(xa, xb, go, weight_shape, padding, dw_dtype, want_db=False, db_dtype=None):
+    """(dW, db or None) of a k=3 Conv3d over cat(xa, xb)."""
+    lib = load()
+    go = go.contiguous()
+    ca = int(xa.shape[1])
+    desc = _cat_desc(xa.shape, xb.shape[1], go.shape, 3, padding, xa.dtype, go.stride())
+    dw = torch.empty(tuple(int(v) for v in weight_shape), device=xa.device, dtype=dw_dtype)
+    db = None
+    if want_db:
+        db = torch.empty((int(weight_shape[0]),), device=xa.device, dtype=db_dtype or dw_dtype)
+    xb_s0 = int(xb.stride(0))
+    ws = _workspace(lib.r3c_conv3d_cat_workspace(ctypes.byref(desc), ca, xb_s0, 2), xa.device, "r3c_conv3d_cat_dw")
+    rc = lib.r3c_conv3d_cat_dw(ctypes.byref(desc), ca, _ptr(xa), _ptr(xb), xb_s0, _ptr(go), _ptr(dw),
+                               _DTYPE_CODE[dw_dtype], _ptr(db), _DTYPE_CODE[db.dtype] if db is not None else R3C_F32,
+                               _ptr(ws), ws.numel(), _stream_handle(xa.device))
+    _check(lib, rc, "r3c_conv3d_cat_dw")
+    return dw, db

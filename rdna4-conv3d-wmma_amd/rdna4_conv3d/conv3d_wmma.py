@@ -451,6 +451,71 @@ class Conv3dWmma(nn.Conv3d):
             return super().forward(x)
         return conv3d_wmma(x, self.weight, self.bias, self.stride, self.padding, self.dilation, 1)
 
+    def forward_cat(self, xa, xb):
+        """self(torch.cat((xa, xb), 1)) without writing the concatenation: a
+        k=3 stride-1 layer on contiguous NCDHW half-precision inputs (or under
+        autocast) reads the two tensors directly and returns the gradients of
+        xa and xb as two tensors.  Anything else concatenates and calls forward."""
+        if not self._cat_native_ok(xa, xb):
+            return self.forward(torch.cat((xa, xb), 1))
+        xa, w, b = _autocast_args(xa, self.weight, self.bias)
+        xb = xb.to(xa.dtype) if xb.dtype != xa.dtype else xb
+        if xa.dtype not in _HALF:
+            return self.forward(torch.cat((xa, xb), 1))
+        w = w.to(xa.dtype) if w.dtype != xa.dtype else w
+        if b is not None and b.dtype != xa.dtype:
+            b = b.to(xa.dtype)
+        _ensure_native(xa.device)
+        return _Conv3dCatFn.apply(xa, xb, w, b, _t3(self.padding))
+
+    def _cat_native_ok(self, xa, xb) -> bool:
+        if (self.groups != 1 or self.padding_mode != "zeros" or isinstance(self.padding, str)
+                or tuple(self.kernel_size) != (3, 3, 3) or _t3(self.stride) != (1, 1, 1)
+                or _t3(self.dilation) != (1, 1, 1) or not _wmma_hw()):
+            return False
+        if not (_native_tensors_ok(xa, xb) and xa.dim() == 5 and xb.dim() == 5):
+            return False
+        if int(xa.shape[1]) + int(xb.shape[1]) != int(self.weight.shape[1]):
+            return False
+        dt = _autocast_dtype() or xa.dtype
+        if dt not in _HALF or not (xa.dtype == xb.dtype and (xa.dtype == dt or _autocast_dtype() is not None)):
+            return False
+        if not _native.cat_tensors_ok(xa, xb):
+            return False
+        return _native.cat_plans_ok(xa, xb, self.weight.shape, _t3(self.padding), dt)
+
+
+class _Conv3dCatFn(torch.autograd.Function):
+    """k=3 Conv3d over cat(xa, xb) on the native kernels (inputs already in the compute dtype)."""
+
+    @staticmethod
+    def forward(ctx, xa, xb, weight, bias, padding):
+        with torch.cuda.device(xa.device):
+            y = _native.conv3d_cat_fwd(xa, xb, weight, bias, padding)
+        ctx.save_for_backward(xa, xb, weight)
+        ctx.padding = padding
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, go):
+        xa, xb, weight = ctx.saved_tensors
+        go = go.to(xa.dtype).contiguous()
+        need_a, need_b_in, need_w, need_bias = ctx.needs_input_grad[:4]
+        dxa = dxb = dw = db = None
+        with torch.cuda.device(xa.device):
+            if need_a or need_b_in:
+                dxa, dxb = _native.conv3d_cat_dx(go, weight, xa.shape, xb.shape, ctx.padding)
+            if need_w or (need_bias and ctx.has_bias):
+                dw, db = _native.conv3d_cat_dw(xa, xb, go, weight.shape, ctx.padding, torch.float32,
+                                               want_db=need_bias and ctx.has_bias,
+                                               db_dtype=_db_dtype(ctx.bias_dtype, xa.dtype))
+                dw = dw.to(weight.dtype) if need_w else None
+                if db is not None and db.dtype != ctx.bias_dtype:
+                    db = db.to(ctx.bias_dtype)
+        return dxa, dxb, dw, db, None
+
 
 # ---------------------------------------------------------------------------
 # ConvTranspose3d k=2 s=2 p=0 (reference conv3d_wmma.py:1446-1595)

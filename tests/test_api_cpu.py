@@ -141,3 +141,13 @@ def test_maxpool_on_cpu_is_maxpool3d():
         assert isinstance(mod, nn.MaxPool3d)
         assert not mod._native_ok(x)
         torch.testing.assert_close(mod(x), ref(x), atol=0, rtol=0)
+
+
+def test_forward_cat_on_cpu_is_conv_of_cat():
+    """Conv3dWmma.forward_cat(a, b) equals the module applied to torch.cat((a, b), 1)
+    wherever the native kernels do not run (here: CPU tensors)."""
+    from rdna4_conv3d import Conv3dWmma
+    torch.manual_seed(0)
+    conv = Conv3dWmma(12, 5, 3, padding=1)
+    a, b = torch.randn(2, 8, 4, 5, 6), torch.randn(2, 4, 4, 5, 6)
+    torch.testing.assert_close(conv.forward_cat(a, b), conv(torch.cat((a, b), 1)), atol=0, rtol=0)

@@ -218,3 +218,36 @@ def test_pool_descriptors_validate_on_host():
     assert call((2, 8, 4, 4, 8), ys=(8 * 16 + 2, 16)) == (U, U)    # y sample stride not a multiple of 4
     assert call((2, 8, 4, 4, 8), dtype=7) == (U, U)
     assert lib.r3c_maxpool2_fwd(None, None, None, None, None) == I
+
+
+def test_cat_workspace_query_decides_on_host():
+    """Conv3d over a channel concatenation: the workspace query accepts k=3
+    NCDHW layers whose three passes have plans (rows of 32-128 positions, a
+    split on the 8-channel blocks) and returns -1 otherwise; bad descriptors
+    are refused before any device call."""
+    import torch
+    lib = _native.load()
+
+    def q(n, ca, cb, co, d, h, w, pass_=2, channels_last=False):
+        x_shape, y_shape = (n, ca, d, h, w), (n, co, d, h, w)  # k=3, padding 1
+        desc = _native._cat_desc(x_shape, cb, y_shape, 3, (1, 1, 1), torch.bfloat16,
+                                 _native._dense_strides(y_shape, False))
+        if channels_last:
+            xs = _native._dense_strides((n, ca + cb, d, h, w), True)
+            for i in range(5):
+                desc.x_strides[i] = xs[i]
+        return lib.r3c_conv3d_cat_workspace(ctypes.byref(desc), ca, cb * d * h * w, pass_)
+
+    for p in (0, 1, 2):
+        assert q(2, 24, 24, 24, 8, 16, 128, pass_=p) >= 0
+        assert q(2, 48, 48, 48, 8, 16, 64, pass_=p) >= 0
+    assert q(2, 12, 12, 24, 8, 16, 64) == -1          # split off the 8-channel blocks
+    assert q(2, 24, 24, 24, 8, 16, 16) == -1          # rows of 16: no row-walking dW plan
+    assert q(2, 24, 24, 24, 8, 16, 64, channels_last=True, pass_=0) == -1
+    assert q(2, 24, 24, 24, 8, 16, 64, pass_=3) == -1
+    desc = _native._cat_desc((2, 24, 8, 16, 64), 24, (2, 24, 8, 16, 64), 3, (1, 1, 1), torch.bfloat16,
+                             _native._dense_strides((2, 24, 8, 16, 64), False))
+    rc = lib.r3c_conv3d_cat_fwd(ctypes.byref(desc), 24, None, None, 24 * 8 * 16 * 64, None, None, None, None, 0, None)
+    assert rc == _native.R3C_INVALID
+    rc = lib.r3c_conv3d_cat_fwd(ctypes.byref(desc), 20, None, None, 24 * 8 * 16 * 64, None, None, None, None, 0, None)
+    assert rc == _native.R3C_UNSUPPORTED

@@ -17,7 +17,8 @@ the native dX keeps them (0.05-0.4), so there the native path must only be at
 least as accurate as stock.
 
 Over 40 steps (bf16): the loss curves of the native model (and of the model
-that also runs the native BatchNorm + ReLU and MaxPool3d(2)) and of stock must
+that also runs the native BatchNorm + ReLU, MaxPool3d(2) and the decoder convs
+over the skip concatenation without torch.cat) and of stock must
 agree within 1e-2 -- a regression bound a wrong gradient exceeds within a few
 steps -- and the north star's own |dloss| <= 1e-3 is recorded as an expected
 failure: two correct bf16 computations of this model already differ by more
@@ -171,7 +172,7 @@ def _curves():
     nat.timing_enable(True)
     nat.timing_collect()
     _, all_native = bench.unet3d_train(Conv3dWmma, ConvTranspose3dWmma, 24, x, labels, STEPS - 3, 3,
-                                       bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma)
+                                       bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma, cat_free=True)
     kinds = {k for _, k, _ in nat.timing_collect()}
     nat.timing_enable(False)
     assert {"row", "wgrad", "bn", "pool"} <= kinds, kinds
