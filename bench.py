@@ -439,6 +439,37 @@ def unet_probe(name: str) -> int:
     return 0
 
 
+def mfma_probe() -> int:
+    """MFMA shape throughput on this GPU (bf16, dense): the library's probe
+    kernel issues independent MFMAs of one shape from every wave; prints one
+    JSON line per (shape, waves per SIMD) with TFLOP/s and the fraction of the
+    published 2.5 PFLOP/s.  The basis for building every k=3 kernel on
+    v_mfma_f32_32x32x16 rather than 16x16x32."""
+    import torch
+    from rdna4_conv3d import _native as nat
+    dev = torch.device("cuda", 0)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 4096
+    for shape, name, flops_per, per_round in ((0, "32x32x16", 32768, 4), (1, "16x16x32", 16384, 8)):
+        for wps in (1, 2, 4):  # waves per SIMD: 4 SIMDs per CU, 4 waves per 256-thread workgroup
+            blocks = cus * wps
+            out = torch.empty(blocks * 256, device=dev, dtype=torch.float32)
+            nat.probe_mfma(shape, blocks, 64, out)  # warm-up
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            nat.probe_mfma(shape, blocks, iters, out)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            flops = blocks * 4 * iters * per_round * flops_per
+            tf = flops / (ms * 1e-3) / 1e12
+            print(json.dumps({"probe": "mfma", "shape": f"v_mfma_f32_{name}_bf16", "waves_per_simd": wps,
+                              "cus": cus, "iters": iters, "ms": round(ms, 3), "tflops": round(tf, 1),
+                              "frac_peak": round(tf / MFMA_PEAK_TFLOPS, 4)}), flush=True)
+    return 0
+
+
 def traffic_probe(name: str, layout: str) -> int:
     """Kernels for an HBM-traffic measurement (run under rocprofv3 --pmc): a
     256 MiB device copy three times (FETCH_SIZE / WRITE_SIZE calibration), then
@@ -491,7 +522,8 @@ def main() -> int:
     ap.add_argument("--probe", default=None, metavar="PASS",
                     help="traffic probe for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB Tensor.copy_ (the "
                          "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd; or "
-                         "unet24[_fused|_stock]: 8 UNet3D training steps for a kernel trace; exits")
+                         "unet24[_fused|_stock]: 8 UNet3D training steps for a kernel trace; or mfma: "
+                         "MFMA shape throughput (32x32x16 vs 16x16x32); exits")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="diagnostic: time the step without the per-launch event hook (no roofline/passes)")
     args = ap.parse_args()
@@ -520,6 +552,8 @@ def main() -> int:
     def L(t):
         return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
 
+    if args.probe == "mfma":
+        return mfma_probe()
     if args.probe and args.probe.startswith("unet"):
         return unet_probe(args.probe)
     if args.probe:
@@ -577,11 +611,18 @@ def main() -> int:
                 avg = sum(main) / len(main)
                 fl = layers[li][4]
                 name = f"k3_{ci}to{co}_{d}x{h}x{w}_{p}"
+                aux_kinds = {}
+                for (t, k), v in per.items():
+                    if t == tag and k != main_kind:
+                        aux_kinds[k] = round(sum(v) / max(1, len(main)) * 1e3, 2)
                 passes[name] = {
                     "kernel_us": round(avg * 1e3, 2),
                     "aux_us": round(aux * 1e3, 2),
+                    "aux_by_kind_us": aux_kinds,
                     "tflops": round(fl / (avg * 1e-3) / 1e12, 1),
                     "frac_mfma": round(fl / (avg * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                    # the whole pass: main kernel plus its weight pack, reduce, copies, split epilogue
+                    "frac_mfma_with_aux": round(fl / ((avg + aux) * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                 }
                 share = avg * len(main)
                 if dominant is None or share > dominant[0]:

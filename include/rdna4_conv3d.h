@@ -243,6 +243,15 @@ int32_t r3c_maxpool2_fwd(const r3c_pool_desc* desc, const void* x, void* y,
 int32_t r3c_maxpool2_bwd(const r3c_pool_desc* desc, const void* dy,
                          const uint8_t* idx, void* dx, void* stream);
 
+/* ---- MFMA shape probe (measurement only) -------------------------------------
+ * No counterpart in the reference.  `blocks` workgroups of 256 threads each
+ * issue `iters` rounds of independent bf16 MFMAs of one shape (0:
+ * v_mfma_f32_32x32x16, 4 per round, 32768 flops each; 1: 16x16x32, 8 per
+ * round, 16384 flops each) and write one float per thread to out
+ * (blocks * 256 floats).  The caller times the launch on `stream`. */
+int32_t r3c_probe_mfma(int32_t shape, int32_t blocks, int32_t iters,
+                       float* out, void* stream);
+
 /* ---- Kernel timing hook (measurement only) ----------------------------------
  * No counterpart in the reference (its benches time whole calls with
  * time.perf_counter, benches/isolated.py:26-34).  While enabled, each kernel

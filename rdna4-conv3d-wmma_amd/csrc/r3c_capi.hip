@@ -1728,6 +1728,15 @@ int32_t r3c_bn_relu_bwd(const r3c_bn_desc* d, const void* dz, const void* y, con
   return check_launch("BatchNorm + ReLU backward");
 }
 
+int32_t r3c_probe_mfma(int32_t shape, int32_t blocks, int32_t iters, float* out, void* stream) {
+  if (shape != 0 && shape != 1) return fail(R3C_INVALID, "probe shape must be 0 (32x32x16) or 1 (16x16x32)");
+  if (blocks < 1 || iters < 1 || !out) return fail(R3C_INVALID, "probe: blocks and iters >= 1, out non-null");
+  int rc = check_device();
+  if (rc) return rc;
+  launch_mfma_probe(shape, blocks, iters, out, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("MFMA probe");
+}
+
 int32_t r3c_maxpool2_fwd(const r3c_pool_desc* d, const void* x, void* y, uint8_t* idx, void* stream) {
   PoolArgs a;
   int rc = pool_setup(d, a);

@@ -306,6 +306,8 @@ void launch_t2dx_pack(const T2dxPackArgs& a, hipStream_t stream);
 void launch_bn_relu_fwd(int dtype, const BnArgs& a, hipStream_t stream);
 void launch_bn_relu_bwd(int dtype, const BnArgs& a, hipStream_t stream);
 // MaxPool3d(2): forward (y, idx) and backward (dx); dtype as the C ABI's codes.
+// MFMA shape probe (r3c_probe.hip): shape 0 32x32x16, 1 16x16x32 (bf16).
+void launch_mfma_probe(int shape, int blocks, int iters, float* out, hipStream_t stream);
 // pass 0 fwd, 1 dX, 2 dW partials; false if O is not 1..4.
 bool launch_skinny(int dtype, int pass, const SkinnyArgs& a, hipStream_t stream);
 void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);

@@ -118,8 +118,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const int seg = it % NSEG, ch = (it / NSEG) % 32, r = it / (32 * NSEG);
     const bool ex = it < NFS;
     frow[k] = ex ? r : -1;
-    frel[k] = 2 * ((fc0 + ch) * fs1 + r * fs3 + 8 * seg);
     fval[k] = ex && fc0 + ch < a.Fc;
+    // A load that is switched off keeps channel 0 in its offset: the product
+    // of a channel past Fc and a large channel stride could leave int32.
+    frel[k] = 2 * ((fval[k] ? fc0 + ch : 0) * fs1 + r * fs3 + 8 * seg);
     fslot[k] = ((ex ? r : 0) * 32 + ch) * P + 8 + 8 * seg;
   }
   // x: it = k NT + tid -> (row r, plane kd, channel, segment), segment fastest.
@@ -133,8 +135,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const bool ex = it < NGS;
     grow[k] = ex ? r : -1;
     gkd[k] = pk;
-    grel[k] = 2 * ((gcl + ch) * gs1 + 8 * seg);
     gval[k] = ex && gc0 + ch < a.Gc;
+    grel[k] = 2 * ((gval[k] ? gcl + ch : 0) * gs1 + 8 * seg);  // as frel
     gslot[k] = (pk * GCW + ch) * P + 8 + 8 * seg;  // plus the ring slot of row r
   }
 

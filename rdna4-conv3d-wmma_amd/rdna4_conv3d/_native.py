@@ -126,6 +126,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_conv3d_cat_dx.argtypes = [D, I32, P, P, P, P, ctypes.c_int64, P, ctypes.c_int64, P]
     lib.r3c_conv3d_cat_dw.restype = I32
     lib.r3c_conv3d_cat_dw.argtypes = [D, I32, P, P, ctypes.c_int64, P, P, I32, P, I32, P, ctypes.c_int64, P]
+    lib.r3c_probe_mfma.restype = I32
+    lib.r3c_probe_mfma.argtypes = [I32, I32, I32, P, P]
     Q = ctypes.POINTER(PoolDesc)
     lib.r3c_maxpool2_fwd.restype = I32
     lib.r3c_maxpool2_fwd.argtypes = [Q, P, P, P, P]
@@ -642,3 +644,10 @@ def conv3d_cat_dw(xa, xb, go, weight_shape, padding, dw_dtype, want_db=False, db
                                _ptr(ws), ws.numel(), _stream_handle(xa.device))
     _check(lib, rc, "r3c_conv3d_cat_dw")
     return dw, db
+
+
+def probe_mfma(shape: int, blocks: int, iters: int, out: torch.Tensor) -> None:
+    """Launch the MFMA shape probe on out's device (see include/rdna4_conv3d.h)."""
+    lib = load()
+    rc = lib.r3c_probe_mfma(int(shape), int(blocks), int(iters), _ptr(out), _stream_handle(out.device))
+    _check(lib, rc, "r3c_probe_mfma")
