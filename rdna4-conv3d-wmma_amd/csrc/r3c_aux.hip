@@ -143,8 +143,9 @@ __device__ __forceinline__ void store_elem(void* base, int64_t i, int dtype, flo
 
 // Element e of the reduce: [0, Fc*taps*Gc) are dW, walked with G fastest
 // (matching the partial layout, so a wave reads consecutive floats); the tail
-// holds db.  split_sum adds splits [s0, s1) of one element in increasing order.
-__device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64_t nw, int s0, int s1) {
+// holds db.  split_sum adds splits s0, s0 + step, ... below s1 of one element
+// in increasing order.
+__device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64_t nw, int s0, int s1, int step = 1) {
   float sum = 0.f;
   if (e < nw) {
     const int gch = (int)(e % a.Gc);
@@ -154,15 +155,15 @@ __device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64
     const size_t stride = (size_t)a.Fpad * a.taps * a.Gpad;
     const float* p = a.part + ((size_t)f * a.taps + tap) * a.Gpad + gch;
 #pragma unroll 8
-    for (int s = s0; s < s1; ++s) sum += p[(size_t)s * stride];
+    for (int s = s0; s < s1; s += step) sum += p[(size_t)s * stride];
   } else {
     const int c = (int)(e - nw);
     if (a.db_mode == 1) {
 #pragma unroll 8
-      for (int s = s0; s < s1; ++s) sum += a.dbpart[(size_t)s * a.Fpad + c];
+      for (int s = s0; s < s1; s += step) sum += a.dbpart[(size_t)s * a.Fpad + c];
     } else if (a.taps == 8) {  // ConvTranspose: the 8 tap partials of a split, loads issued together
 #pragma unroll 4
-      for (int s = s0; s < s1; ++s) {
+      for (int s = s0; s < s1; s += step) {
         const float* q = a.dbpart + (size_t)s * 8 * a.Gpad + c;
         float t = 0.f;
 #pragma unroll
@@ -170,7 +171,7 @@ __device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64
         sum += t;
       }
     } else {
-      for (int s = s0; s < s1; ++s) {
+      for (int s = s0; s < s1; s += step) {
         float t = 0.f;
         for (int tap = 0; tap < a.taps; ++tap) t += a.dbpart[((size_t)s * a.taps + tap) * a.Gpad + c];
         sum += t;
@@ -180,28 +181,13 @@ __device__ __forceinline__ float split_sum(const ReduceArgs& a, int64_t e, int64
   return sum;
 }
 
-// First level: group blockIdx.y sums splits [y*kReduceGroup, (y+1)*kReduceGroup).
-__global__ __launch_bounds__(256) void wgrad_reduce_groups_kernel(const ReduceArgs a, int64_t nw, int64_t ne) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= ne) return;
-  const int s0 = blockIdx.y * kReduceGroup;
-  const int s1 = s0 + kReduceGroup < a.nsplit ? s0 + kReduceGroup : a.nsplit;
-  a.lvl2[(size_t)blockIdx.y * ne + e] = split_sum(a, e, nw, s0, s1);
-}
-
-// Last level: the group sums in increasing group order (or, with one group,
-// the splits themselves), converted to the output dtype.  Bitwise
-// reproducible run to run: every sum has a fixed order.
+// Few splits (at most 32): one thread per element adds them in
+// split order and converts to the output dtype.  Bitwise reproducible run to
+// run: every sum has a fixed order.
 __global__ __launch_bounds__(256) void wgrad_reduce_final_kernel(const ReduceArgs a, int64_t nw, int64_t ne) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= ne) return;
-  float tot;
-  if (a.ngroups <= 1) {
-    tot = split_sum(a, e, nw, 0, a.nsplit);
-  } else {
-    tot = 0.f;
-    for (int gi = 0; gi < a.ngroups; ++gi) tot += a.lvl2[(size_t)gi * ne + e];
-  }
+  const float tot = split_sum(a, e, nw, 0, a.nsplit);
   if (e < nw) {
     const int gch = (int)(e % a.Gc);
     const int64_t r = e / a.Gc;
@@ -213,14 +199,55 @@ __global__ __launch_bounds__(256) void wgrad_reduce_final_kernel(const ReduceArg
   }
 }
 
+// One launch for many splits: a workgroup owns 256 / SG consecutive elements,
+// SG threads per element each add every SG-th split in increasing order, and
+// thread 0 of each element adds the SG sums in order.  Bitwise reproducible.
+template <int SG>
+__global__ __launch_bounds__(256) void wgrad_reduce_tree_kernel(const ReduceArgs a, int64_t nw, int64_t ne) {
+  constexpr int EPB = 256 / SG;
+  __shared__ float sh[256];
+  const int t = threadIdx.x;
+  const int el = t % EPB, sg = t / EPB;
+  const int64_t e = (int64_t)blockIdx.x * EPB + el;
+  sh[t] = e < ne ? split_sum(a, e, nw, sg, a.nsplit, SG) : 0.f;
+  __syncthreads();
+  if (sg != 0 || e >= ne) return;
+  float tot = 0.f;
+#pragma unroll
+  for (int j = 0; j < SG; ++j) tot += sh[j * EPB + el];
+  if (e < nw) {
+    const int gch = (int)(e % a.Gc);
+    const int64_t r = e / a.Gc;
+    const int tap = (int)(r % a.taps);
+    const int f = (int)(r / a.taps);
+    store_elem<float>(a.dw, ((int64_t)f * a.Gc + gch) * a.taps + tap, a.dw_dtype, tot);
+  } else {
+    store_elem<float>(a.db, e - nw, a.db_dtype, tot);
+  }
+}
+
+template <int SG>
+void launch_tree(const ReduceArgs& a, int64_t nw, int64_t ne, hipStream_t stream) {
+  const unsigned blocks = (unsigned)((ne + 256 / SG - 1) / (256 / SG));
+  hipLaunchKernelGGL(wgrad_reduce_tree_kernel<SG>, dim3(blocks), dim3(256), 0, stream, a, nw, ne);
+}
+
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream) {
   const int64_t nw = (int64_t)a.Fc * a.taps * a.Gc;
   const int ndb = a.db_mode == 1 ? a.Fc : (a.db_mode == 2 ? a.Gc : 0);
   const int64_t ne = nw + ndb;
-  const unsigned blocks = (unsigned)((ne + 255) / 256);
-  if (a.ngroups > 1)
-    hipLaunchKernelGGL(wgrad_reduce_groups_kernel, dim3(blocks, (unsigned)a.ngroups), dim3(256), 0, stream, a, nw, ne);
-  hipLaunchKernelGGL(wgrad_reduce_final_kernel, dim3(blocks), dim3(256), 0, stream, a, nw, ne);
+  if (a.nsplit <= 32) {  // one thread per element
+    const unsigned blocks = (unsigned)((ne + 255) / 256);
+    hipLaunchKernelGGL(wgrad_reduce_final_kernel, dim3(blocks), dim3(256), 0, stream, a, nw, ne);
+    return;
+  }
+  // Large partial sets are read at HBM speed only while a wave's load covers
+  // long runs of one split row (256 / SG consecutive elements): the fewest
+  // threads per element that keep each thread at 16 splits or so.
+  if (a.nsplit <= 128) launch_tree<8>(a, nw, ne, stream);
+  else if (a.nsplit <= 256) launch_tree<16>(a, nw, ne, stream);
+  else if (a.nsplit <= 512) launch_tree<32>(a, nw, ne, stream);
+  else launch_tree<64>(a, nw, ne, stream);
 }
 
 }  // namespace r3c

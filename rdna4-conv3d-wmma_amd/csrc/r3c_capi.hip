@@ -770,6 +770,63 @@ SkinnyArgs skinny_args(const r3c_conv_desc* d) {
   return a;
 }
 
+// Conv3d k=3 with one input channel (r3c_stem.hip): input rows w-contiguous
+// and 16-byte aligned (W % 8 == 0, at most kStemMaxW), padding at most 2, at
+// most kStemMaxCout output channels.  dW also reads dY rows as 16-byte
+// vectors (ow-contiguous, aligned, OW % 16 == 0).  Pointer alignment is
+// checked by the caller.
+bool stem_ok(const r3c_conv_desc* d, bool dw) {
+  if (d->kernel != 3 || d->cin != 1 || d->cout > kStemMaxCout) return false;
+  if (d->pad_d > 2 || d->pad_h > 2 || d->pad_w > 2) return false;
+  if (d->w % 8 || d->w > kStemMaxW || d->ow > kStemMaxW) return false;
+  const int64_t* xs = d->x_strides;
+  if (xs[4] != 1 || xs[3] % 8 || xs[2] % 8 || xs[0] % 8) return false;
+  if ((int64_t)d->n * d->od * cdiv(d->oh, kStemRows) >= (1ll << 31)) return false;
+  if (dw) {
+    const int64_t* ys = d->y_strides;
+    if (ys[4] != 1 || ys[3] % 8 || ys[2] % 8 || ys[1] % 8 || ys[0] % 8 || d->ow % 16) return false;
+  }
+  return true;
+}
+
+constexpr int kStemSplits = 1024;  // dW partials (workgroups), at most
+
+StemArgs stem_args(const r3c_conv_desc* d) {
+  StemArgs a;
+  memset(&a, 0, sizeof a);
+  a.xs0 = d->x_strides[0];
+  a.xs2 = d->x_strides[2];
+  a.xs3 = d->x_strides[3];
+  for (int i = 0; i < 5; ++i) (&a.ys0)[i] = d->y_strides[i];
+  a.D = d->d;
+  a.H = d->h;
+  a.W = d->w;
+  a.OD = d->od;
+  a.OH = d->oh;
+  a.OW = d->ow;
+  a.pd = d->pad_d;
+  a.ph = d->pad_h;
+  a.pw = d->pad_w;
+  a.Cout = d->cout;
+  // Row pitch: data at [8, 8 + W), zeros around it, and room for the reads of
+  // the last 32-position tile (up to 2 past the row, plus the kw shifts).
+  a.P = (int32_t)((std::max<int64_t>(d->w, cdiv(d->ow, 32) * 32) + 18 + 7) / 8 * 8);
+  a.nrb = (int32_t)cdiv(d->oh, kStemRows);
+  a.njobs = d->n * d->od * a.nrb;
+  a.nsplit = std::min(a.njobs, kStemSplits);
+  return a;
+}
+
+// Dynamic LDS: the staged input rows; dW reuses them for the 4 waves'
+// accumulators, the forward appends each wave's output block (32 channels x
+// 72 positions per channel block) when it stores positions 8 at a time.
+size_t stem_lds(const StemArgs& a, bool dw) {
+  const int nb = a.Cout <= 32 ? 1 : 2;
+  const size_t tile = (size_t)kStemXRows * a.P * 2;
+  if (dw) return std::max(tile, (size_t)kStemRows * nb * 16 * 64 * 4);
+  return tile + (a.yvec8 ? (size_t)kStemRows * nb * 32 * 72 * 2 : 0);
+}
+
 bool aligned16_all(std::initializer_list<const void*> ps) {
   for (const void* p : ps)
     if (reinterpret_cast<uintptr_t>(p) & 15) return false;
@@ -804,6 +861,25 @@ struct CatSpec {
 
 int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, const void* bias, void* dst, void* ws,
             int64_t ws_bytes, void* stream, const CatSpec* cat = nullptr) {
+  if (!cat && op == OP_CONV_FWD && stem_ok(d, false) && aligned16_all({src}) && src && dst && w) {
+    int rc = check_device();
+    if (rc) return rc;
+    StemArgs a = stem_args(d);
+    a.x = static_cast<const uint16_t*>(src);
+    a.w = static_cast<const uint16_t*>(w);
+    a.b = static_cast<const uint16_t*>(bias);
+    a.y = static_cast<uint16_t*>(dst);
+    a.yvec4 = a.ys1 == 1 && a.Cout % 4 == 0 && a.ys0 % 4 == 0 && a.ys2 % 4 == 0 && a.ys3 % 4 == 0 &&
+              a.ys4 % 4 == 0 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0;
+    a.yvec8 = a.ys4 == 1 && a.OW % 8 == 0 && a.ys0 % 8 == 0 && a.ys1 % 8 == 0 && a.ys2 % 8 == 0 &&
+              a.ys3 % 8 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    TimedLaunch tl(KIND_ROW, s);
+    const bool launched = launch_stem(d->dtype, 0, a, stem_lds(a, false), s);
+    tl.end();
+    if (!launched) return fail(R3C_UNSUPPORTED, "no one-channel k=3 instantiation for %d output channels", a.Cout);
+    return check_launch("one-channel k=3 forward");
+  }
   if (!cat && (op == OP_CONV_FWD || op == OP_CONV_DX) && skinny_ok(d) && aligned16_all({src, dst}) && src && dst && w) {
     int rc = check_device();
     if (rc) return rc;
@@ -918,7 +994,7 @@ int run_row(const r3c_conv_desc* d, int op, const void* src, const void* w, cons
 // Weight-gradient plan (Conv3d dW k1/k3, ConvTranspose dW)
 // ---------------------------------------------------------------------------
 struct WgPlan {
-  int mode, cbw, taps, ngroups;
+  int mode, cbw, taps;
   int pw;              // 1: register-direct single-tap kernel (r3c_pwdw.h), fields below
   int tr, tc, nj;
   PwdwArgs pa;
@@ -926,7 +1002,7 @@ struct WgPlan {
            // 3: k=3, G transposed from w-contiguous in the kernel; 5: k=3 row-walking kernel (r3c_wgrow.h)
   WgArgs a;
   size_t lds;
-  int64_t part_bytes, dbpart_bytes, lvl2_bytes, nelem;
+  int64_t part_bytes, dbpart_bytes;
   int64_t fcopy_bytes, gcopy_bytes;  // > 0: that operand is first copied to NDHWC
 };
 
@@ -1007,9 +1083,6 @@ bool plan_pwdw(const r3c_conv_desc* d, bool transpose, WgPlan& p) {
   p.mode = transpose ? MODE_T2DW : MODE_K1;
   p.part_bytes = align256(a.nsplit * per_split);
   p.dbpart_bytes = align256((int64_t)a.nsplit * std::max(w.Fc, 8 * w.Gc) * 4);
-  p.ngroups = cdiv(a.nsplit, kReduceGroup);
-  p.nelem = (int64_t)w.Fc * p.taps * w.Gc + std::max(w.Fc, w.Gc);
-  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
   p.fcopy_bytes = p.gcopy_bytes = 0;
   p.lds = 0;
   return true;
@@ -1183,10 +1256,6 @@ void plan_wgrad(const r3c_conv_desc* d, bool transpose, WgPlan& p, bool allow_pw
   p.lds = (size_t)lds;
   p.part_bytes = align256(nsplit * per_split);
   p.dbpart_bytes = align256(nsplit * (int64_t)std::max(a.Fpad, p.taps * a.Gpad) * 4);
-  // Two-level reduce: group sums of kReduceGroup splits, then their sum.
-  p.ngroups = cdiv(nsplit, kReduceGroup);
-  p.nelem = (int64_t)a.Fc * p.taps * a.Gc + std::max(a.Fc, a.Gc);
-  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
 }
 
 // Register-direct single-tap weight gradient, then the shared fixed-order reduce.
@@ -1220,8 +1289,6 @@ int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void
   r.dw_dtype = dw_dtype;
   r.db_dtype = db_dtype;
   r.db_mode = a.db_mode;
-  r.ngroups = p.ngroups;
-  r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
   {
     TimedLaunch tr(KIND_REDUCE, s);
     launch_wgrad_reduce(r, s);
@@ -1232,17 +1299,25 @@ int run_pwdw(const r3c_conv_desc* d, bool transpose, const WgPlan& p, const void
 
 // Why a weight-gradient plan cannot run (nullptr: it can); shared with the
 // workspace query.
-// dW partials of the k=1 skinny kernel: one split per 1024 position groups, at most 1024.
+// dW partials of the k=1 skinny kernel: one split per 512 position groups
+// (two per thread, loaded together), at most 4096.
 void plan_skinny_dw(const r3c_conv_desc* d, WgPlan& p) {
   const SkinnyArgs s = skinny_args(d);
-  const int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(1024, s.ngroups / 1024));
+  const int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(4096, cdiv(s.ngroups, 512)));
   p.a.nsplit = (int32_t)nsplit;
   p.taps = 1;
   p.part_bytes = align256(nsplit * (int64_t)s.O * s.C * 4);
   p.dbpart_bytes = align256(nsplit * (int64_t)s.O * 4);
-  p.ngroups = cdiv(nsplit, kReduceGroup);
-  p.nelem = (int64_t)s.O * s.C + std::max(s.O, s.C);
-  p.lvl2_bytes = p.ngroups > 1 ? align256((int64_t)p.ngroups * p.nelem * 4) : 0;
+  p.fcopy_bytes = p.gcopy_bytes = 0;
+}
+
+// dW partials of the one-channel k=3 kernel: one per workgroup.
+void plan_stem_dw(const r3c_conv_desc* d, WgPlan& p) {
+  const StemArgs s = stem_args(d);
+  p.a.nsplit = s.nsplit;
+  p.taps = 27;
+  p.part_bytes = align256((int64_t)s.nsplit * s.Cout * 27 * 4);
+  p.dbpart_bytes = align256((int64_t)s.nsplit * s.Cout * 4);
   p.fcopy_bytes = p.gcopy_bytes = 0;
 }
 
@@ -1254,7 +1329,7 @@ const char* wgrad_plan_reject(const WgPlan& p) {
 }
 
 int64_t wgrad_plan_ws(const WgPlan& p) {
-  return p.part_bytes + p.dbpart_bytes + p.lvl2_bytes + p.fcopy_bytes + p.gcopy_bytes;
+  return p.part_bytes + p.dbpart_bytes + p.fcopy_bytes + p.gcopy_bytes;
 }
 
 int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void* dy, void* dw, int dw_dtype, void* db,
@@ -1262,9 +1337,15 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   // The register-direct single-tap kernel loads 16-byte vectors; other
   // alignments take the LDS-staged kernel, which stages any alignment.
   const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0;
-  if (!cat && !transpose && skinny_ok(d) && al16 && x && dy && dw && ws) {
+  // Dedicated kernels: k=1 with at most 4 output channels (skinny), k=3 with
+  // one input channel (stem).  Both write fp32 partials [split][Cout][taps][Cin]
+  // (+ db partials [split][Cout]) for the split-ordered reduce.
+  const bool skinny = !cat && !transpose && skinny_ok(d) && al16;
+  const bool stem = !cat && !transpose && !skinny && stem_ok(d, true) && al16;
+  if ((skinny || stem) && x && dy && dw && ws) {
     WgPlan p;
-    plan_skinny_dw(d, p);
+    if (stem) plan_stem_dw(d, p);
+    else plan_skinny_dw(d, p);
     const int64_t need = wgrad_plan_ws(p);
     if (ws_bytes < need)
       return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
@@ -1274,37 +1355,48 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
     int rc = check_device();
     if (rc) return rc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    SkinnyArgs a = skinny_args(d);
-    a.x = const_cast<uint16_t*>(static_cast<const uint16_t*>(x));
-    a.y = const_cast<uint16_t*>(static_cast<const uint16_t*>(dy));
-    a.part = static_cast<float*>(ws);
-    a.dbpart = db ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes) : nullptr;
-    a.nsplit = p.a.nsplit;
+    float* part = static_cast<float*>(ws);
+    float* dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
     {
       TimedLaunch tl(KIND_WGRAD, s);
-      const bool launched = launch_skinny(d->dtype, 2, a, s);
+      bool launched;
+      if (stem) {
+        StemArgs a = stem_args(d);
+        a.x = static_cast<const uint16_t*>(x);
+        a.dy = static_cast<const uint16_t*>(dy);
+        a.part = part;
+        a.dbpart = db ? dbpart : nullptr;
+        a.nsplit = p.a.nsplit;
+        launched = launch_stem(d->dtype, 2, a, stem_lds(a, true), s);
+      } else {
+        SkinnyArgs a = skinny_args(d);
+        a.x = const_cast<uint16_t*>(static_cast<const uint16_t*>(x));
+        a.y = const_cast<uint16_t*>(static_cast<const uint16_t*>(dy));
+        a.part = part;
+        a.dbpart = db ? dbpart : nullptr;
+        a.nsplit = p.a.nsplit;
+        launched = launch_skinny(d->dtype, 2, a, s);
+      }
       tl.end();
-      if (!launched) return fail(R3C_UNSUPPORTED, "no k=1 skinny instantiation for %d output channels", a.O);
+      if (!launched) return fail(R3C_UNSUPPORTED, "no dedicated dW instantiation for %d output channels", d->cout);
     }
-    rc = check_launch("k=1 skinny dW");
+    rc = check_launch(stem ? "one-channel k=3 dW" : "k=1 skinny dW");
     if (rc) return rc;
     ReduceArgs r;
     memset(&r, 0, sizeof r);
-    r.part = a.part;
-    r.dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes);
+    r.part = part;
+    r.dbpart = dbpart;
     r.dw = dw;
     r.db = db;
-    r.nsplit = a.nsplit;
-    r.Fc = a.O;
-    r.Gc = a.C;
-    r.taps = 1;
-    r.Fpad = a.O;
-    r.Gpad = a.C;
+    r.nsplit = p.a.nsplit;
+    r.Fc = d->cout;
+    r.Gc = d->cin;
+    r.taps = p.taps;
+    r.Fpad = d->cout;
+    r.Gpad = d->cin;
     r.dw_dtype = dw_dtype;
     r.db_dtype = db_dtype;
     r.db_mode = db ? 1 : 0;
-    r.ngroups = p.ngroups;
-    r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
     {
       TimedLaunch tr(KIND_REDUCE, s);
       launch_wgrad_reduce(r, s);
@@ -1339,7 +1431,7 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
     a.g2_bytes = (uint32_t)(2 * (int64_t)(d->cin - cat->ca) * a.gs[1]);
   }
   {
-    char* copies = static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes + p.lvl2_bytes;
+    char* copies = static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes;
     if (p.fcopy_bytes) {
       rc = copy_to_channels_last(a.fsrc, copies, d->n, a.Fc, a.Rd, a.Rh, a.Rw, s);
       if (rc) return rc;
@@ -1399,8 +1491,6 @@ int run_wgrad(const r3c_conv_desc* d, bool transpose, const void* x, const void*
   r.dw_dtype = dw_dtype;
   r.db_dtype = db_dtype;
   r.db_mode = a.db_mode;
-  r.ngroups = p.ngroups;
-  r.lvl2 = p.ngroups > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.part_bytes + p.dbpart_bytes) : nullptr;
   {
     TimedLaunch tr(KIND_REDUCE, s);
     launch_wgrad_reduce(r, s);
@@ -1519,6 +1609,11 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   if (!transpose && skinny_ok(d)) {
     WgPlan k;
     plan_skinny_dw(d, k);
+    need = std::max<int64_t>(need, wgrad_plan_ws(k));
+  }
+  if (!transpose && stem_ok(d, true)) {
+    WgPlan k;
+    plan_stem_dw(d, k);
     need = std::max<int64_t>(need, wgrad_plan_ws(k));
   }
   // Unaligned sources take the plan without copies or the kw-shift kernel.

@@ -194,16 +194,13 @@ struct T2dxPackArgs {
 struct ReduceArgs {
   const float* part;
   const float* dbpart;
-  float* lvl2;            // [ngroups][nelem] group sums (two-level reduce only)
   void* dw;
   void* db;
   int32_t nsplit, Fc, Gc, taps, Fpad, Gpad;
   int32_t dw_dtype, db_dtype;
   int32_t db_mode;        // 0 none, 1 from F partials, 2 from G partials
-  int32_t ngroups;        // split groups of kReduceGroup; 1 = single pass straight to dW / db
 };
 
-constexpr int kReduceGroup = 32;  // splits summed per thread in the first reduce level
 
 struct PackArgs {
   const uint16_t* w;
@@ -271,6 +268,36 @@ struct SkinnyArgs {
   int32_t C, O, nsplit;
 };
 
+// Conv3d k=3 with one input channel (a volume's first layer): forward and
+// dW + db as dedicated kernels (r3c_stem.hip).  A job is one output plane's
+// block of kStemRows consecutive output rows; its workgroup stages the 3 x
+// (kStemRows + 2) input rows those rows read into LDS, each row at element
+// offset 8 of a zero-padded pitch.
+constexpr int kStemRows = 4;                       // output rows per job (one wave each)
+constexpr int kStemXRows = 3 * (kStemRows + 2);    // staged input rows per job
+constexpr int kStemMaxW = 512;                     // widest input row
+constexpr int kStemMaxCout = 64;                   // output channels (two 32-wide blocks)
+struct StemArgs {
+  const uint16_t* x;     // [n][1][D][H][W], w contiguous, rows 16-byte aligned
+  const uint16_t* w;     // [Cout][27] (OIDHW with one input channel)
+  const uint16_t* b;     // fwd: [Cout] or null
+  uint16_t* y;           // fwd: output
+  const uint16_t* dy;    // dW: output gradient, ow contiguous, rows 16-byte aligned
+  float* part;           // dW: [nsplit][Cout][27] partial sums
+  float* dbpart;         // dW: [nsplit][Cout] or null
+  int64_t xs0, xs2, xs3;              // x strides (n, d, h) in elements
+  int64_t ys0, ys1, ys2, ys3, ys4;    // y / dy strides (n, c, d, h, w)
+  int32_t D, H, W, OD, OH, OW, pd, ph, pw;
+  int32_t Cout;
+  int32_t P;             // LDS row pitch (elements, multiple of 8)
+  int32_t nrb;           // row blocks per output plane
+  int32_t njobs;         // n * OD * nrb
+  int32_t nsplit;        // dW: workgroups (one partial each)
+  int32_t yvec4;         // fwd: 1 = channels contiguous, 4 channels per 8-byte store
+  int32_t yvec8;         // fwd: 1 = positions contiguous and 16-byte aligned rows, OW % 8 == 0:
+                         //      8 positions per 16-byte store (through LDS)
+};
+
 struct PoolArgs {
   const void* x;          // forward input
   void* y;                // forward output
@@ -291,7 +318,7 @@ bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, i
 bool launch_wgrad(int dtype, int mode, int cbw, int cl, int fl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
-// One pass (ngroups == 1) or two (group sums into lvl2, then their fixed-order sum).
+// One launch: a thread per element (few splits) or a fixed-shape tree over the splits.
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 // Row-walking k=3 weight gradient (r3c_wgrow.h); false if no instantiation for (gcw, W).
 bool launch_wgrow(int dtype, int gcw, int w, const WgArgs& a, hipStream_t stream);
@@ -310,6 +337,8 @@ void launch_bn_relu_bwd(int dtype, const BnArgs& a, hipStream_t stream);
 void launch_mfma_probe(int shape, int blocks, int iters, float* out, hipStream_t stream);
 // pass 0 fwd, 1 dX, 2 dW partials; false if O is not 1..4.
 bool launch_skinny(int dtype, int pass, const SkinnyArgs& a, hipStream_t stream);
+// pass 0 = forward, 2 = dW + db; false when Cout has no instantiation.
+bool launch_stem(int dtype, int pass, const StemArgs& a, size_t lds, hipStream_t stream);
 void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);
 void launch_maxpool2_bwd(int dtype, const PoolArgs& a, hipStream_t stream);
 

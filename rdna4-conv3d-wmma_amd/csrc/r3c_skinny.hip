@@ -12,9 +12,10 @@
 //   dX : dx[c][p] = sum_o w[o][c] dy[o][p]           (_dgrad_k1_scale_kernel,
 //                                                     src/rdna4_conv3d/conv3d_wmma.py:761-785)
 //   dW : dw[o][c] = sum_p dy[o][p] x[c][p], db[o] = sum_p dy[o][p]
-// dW: workgroup s owns a fixed, contiguous range of position groups; it sums
-// each channel block of 8 in registers, then over its 256 threads in a fixed
-// order (LDS), and writes partials [s][O][1][C] (+ [s][O] for db) that the
+// dW: workgroup (s, b) owns a fixed, contiguous range s of position groups
+// and channel block b of 8; it sums in registers, then over its 256 threads
+// in a fixed shape (a butterfly per wave, the 4 waves in order), and writes
+// partials [s][O][1][C] (+ [s][O] for db, from block 0) that the
 // weight-gradient reduce adds in split order: deterministic.
 #include "r3c_device.h"
 #include "r3c_kernels.h"
@@ -112,57 +113,76 @@ __global__ __launch_bounds__(256) void skinny_dx_kernel(const SkinnyArgs a) {
 template <typename T, int O>
 __global__ __launch_bounds__(256) void skinny_dw_kernel(const SkinnyArgs a) {
   constexpr int NV = O * 8 + O;  // per thread: 8 channels x O, and db
-  __shared__ float red[256 * NV];
+  __shared__ float red[4 * NV];
   const int s = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t g0 = ((int64_t)s * a.ngroups) / a.nsplit;
   const int64_t g1 = ((int64_t)(s + 1) * a.ngroups) / a.nsplit;
   float* part = a.part + (size_t)s * O * a.C;
-  for (int cb = 0; cb < a.C; cb += 8) {
-    float acc[O][8], dba[O];
+  {
+    // One channel block per workgroup row: every block streams at once (a
+    // loop over the blocks would drain the whole grid's loads once per block).
+    const int cb = 8 * (int)blockIdx.y;
+    float acc[NV];
 #pragma unroll
-    for (int o = 0; o < O; ++o) {
-      dba[o] = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) acc[o][k] = 0.f;
-    }
+    for (int v = 0; v < NV; ++v) acc[v] = 0.f;
     const int nc = a.C - cb < 8 ? a.C - cb : 8;
-    for (int64_t g = g0 + threadIdx.x; g < g1; g += 256) {
-      int n;
-      int64_t p;
-      group_at(a, g, n, p);
-      const uint16_t* dy = a.y + n * a.ys0 + p;
-      const uint16_t* x = a.x + n * a.xs0 + p + (int64_t)cb * a.xs1;
-      float gv[O][8];
+    // Two position groups per iteration, every load of both issued before
+    // any arithmetic (a split holds few groups per thread, so the loads of
+    // one iteration are most of what the thread ever has in flight).
+    for (int64_t g = g0 + threadIdx.x; g < g1; g += 512) {
+      uint4 dq[2][O], xq[2][8];
 #pragma unroll
-      for (int o = 0; o < O; ++o) {
-        unpack8<T>(*reinterpret_cast<const uint4*>(dy + o * a.ys1), gv[o]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dba[o] += gv[o][e];
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (k >= nc) break;
-        float v[8];
-        unpack8<T>(*reinterpret_cast<const uint4*>(x + k * a.xs1), v);
+      for (int u = 0; u < 2; ++u) {
+        const int64_t gu = g + 256 * u;
+        const bool live = gu < g1;
+        int n;
+        int64_t p;
+        group_at(a, live ? gu : g, n, p);
+        const uint16_t* dy = a.y + n * a.ys0 + p;
+        const uint16_t* x = a.x + n * a.xs0 + p + (int64_t)cb * a.xs1;
 #pragma unroll
         for (int o = 0; o < O; ++o)
+          dq[u][o] = live ? *reinterpret_cast<const uint4*>(dy + o * a.ys1) : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[o][k] = fmaf(gv[o][e], v[e], acc[o][k]);
+        for (int k = 0; k < 8; ++k)
+          xq[u][k] = (live && k < nc) ? *reinterpret_cast<const uint4*>(x + k * a.xs1) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float gv[O][8];
+#pragma unroll
+        for (int o = 0; o < O; ++o) {
+          unpack8<T>(dq[u][o], gv[o]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[O * 8 + o] += gv[o][e];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (k >= nc) break;
+          float v[8];
+          unpack8<T>(xq[u][k], v);
+#pragma unroll
+          for (int o = 0; o < O; ++o)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[o * 8 + k] = fmaf(gv[o][e], v[e], acc[o * 8 + k]);
+        }
       }
     }
-    // Sum over the workgroup's threads in thread order.
-    float* mine = red + threadIdx.x * NV;
+    // Fixed-shape reduction (deterministic): a butterfly over the wave's 64
+    // lanes (both partners of a step form the same sum), then the 4 waves in
+    // order.
 #pragma unroll
-    for (int o = 0; o < O; ++o) {
+    for (int off = 32; off >= 1; off >>= 1)
 #pragma unroll
-      for (int k = 0; k < 8; ++k) mine[o * 8 + k] = acc[o][k];
-      mine[O * 8 + o] = dba[o];
-    }
+      for (int v = 0; v < NV; ++v) acc[v] += __shfl_xor(acc[v], off);
+    if (lane == 0)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) red[wave * NV + v] = acc[v];
     __syncthreads();
     if (threadIdx.x < NV) {
-      float t = 0.f;
-      for (int i = 0; i < 256; ++i) t += red[i * NV + threadIdx.x];
       const int v = threadIdx.x;
+      const float t = ((red[v] + red[NV + v]) + red[2 * NV + v]) + red[3 * NV + v];
       if (v < O * 8) {
         const int o = v / 8, k = v % 8;
         if (k < nc) part[o * a.C + cb + k] = t;
@@ -182,7 +202,7 @@ void launch_o(int pass, const SkinnyArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.ngroups + 255) / 256);
   if (pass == 0) hipLaunchKernelGGL((skinny_fwd_kernel<T, O>), dim3(blocks), dim3(256), 0, s, a);
   else if (pass == 1) hipLaunchKernelGGL((skinny_dx_kernel<T, O>), dim3(blocks), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((skinny_dw_kernel<T, O>), dim3((unsigned)a.nsplit), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((skinny_dw_kernel<T, O>), dim3((unsigned)a.nsplit, (unsigned)((a.C + 7) / 8)), dim3(256), 0, s, a);
 }
 template <typename T>
 bool launch_t(int pass, const SkinnyArgs& a, hipStream_t s) {

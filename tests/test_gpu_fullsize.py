@@ -8,7 +8,7 @@ bench makes, and compared with PyTorch's fp32 convolution on the GPU computed
 from the same rounded inputs (F.conv3d, torch.nn.grad.conv3d_input /
 conv3d_weight, F.conv_transpose3d + autograd; the float64 CPU path would take
 minutes here).  At these sizes this pins the plans the small-shape tests never
-reach: the 256-split two-level dW reduce and the staged NCDHW halo of the
+reach: the 256-split dW reduce and the staged NCDHW halo of the
 24-channel layer, the halved split counts of the 96 / 192-channel dW, the
 row kernel's split K at 192 channels, the register-direct k=1 and
 ConvTranspose dW and ConvTranspose dX.  Tolerances (north star):

@@ -70,6 +70,14 @@ CONV_CASES = [
     (2, 24, 24, 16, 64, 64, 3, 1),   # more tiles than CUs: multi-job workgroups, no split K
     (2, 20, 24, 18, 70, 40, 3, 1),   # the same with ragged channels and box edges
     (2, 1, 24, 16, 64, 64, 3, 1),    # one source channel (the first UNet layer)
+    # One source channel: the dedicated kernels (r3c_stem.hip).  Forward with
+    # pad 0 (a partial 32-position tile) and pad 2 with two output-channel
+    # blocks (dW on the general kernels: OW % 16 != 0); dW with two channel
+    # blocks and a partial row block; more dW jobs than workgroups.
+    (1, 1, 16, 6, 9, 24, 3, 0),
+    (1, 1, 40, 5, 7, 16, 3, 2),
+    (1, 1, 40, 6, 10, 32, 3, 1),
+    (4, 1, 32, 40, 42, 128, 3, 1),
     # NCDHW rows of 128 / 64 positions with enough boxes: full-width tap boxes
     # (whole rows, 2 x 4 per box) with ragged d and h edges, and the
     # row-walking dW over columns of odd length
@@ -172,11 +180,12 @@ def test_convt_native_parity(case, layout, dtype):
 
 # Shapes that take the scheduling branches: split K in the row kernel (fewer
 # output tiles than CUs), the NDHWC copy of a low-channel NCDHW operand, and a
-# many-split weight-gradient reduce (two-level).
+# many-split weight-gradient reduce (the tree-shaped single launch).
 DETERMINISM_CASES = [
     (1, 192, 192, 4, 8, 16, 3, 1),   # row kernel split K (fwd and dX)
-    (2, 24, 24, 16, 32, 32, 3, 1),   # NCDHW copy path; dW with two-level reduce
-    (2, 24, 48, 8, 16, 32, 1, 0),    # k=1: register-direct dW (NCDHW) with a two-level reduce
+    (2, 24, 24, 16, 32, 32, 3, 1),   # NCDHW copy path; dW with a many-split reduce
+    (2, 24, 48, 8, 16, 32, 1, 0),    # k=1: register-direct dW (NCDHW) with a many-split reduce
+    (4, 1, 24, 40, 42, 128, 3, 1),   # one source channel: dedicated kernels, 1024 dW partials
 ]
 
 
