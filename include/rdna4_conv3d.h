@@ -113,6 +113,25 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
                       void* dw, int32_t dw_dtype, void* db, int32_t db_dtype,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Conv3d with stride > 1 (downsampling) ----------------------------------
+ * The reference admits stride 1 only (_geom_ok, src/rdna4_conv3d/
+ * conv3d_wmma.py:89-95) and sends strided convolutions to F.conv3d /
+ * torch.nn.grad (conv3d_wmma.py:1233-1319 fallback legs); these entry points
+ * replace those legs.  `stride` points to (sd, sh, sw), each 1 .. 8; `desc`
+ * is a Conv3d descriptor whose output dims are (in + 2 pad - k) / stride + 1,
+ * kernel 1 or 3, any x / y strides.  Forward and dX: a direct kernel (tiles
+ * of one residue class of w for dX); dW + db: dY scattered onto the stride-1
+ * output grid, then the stride-1 weight-gradient kernels (deterministic).
+ * pass: 0 forward, 1 dX, 2 dW; the query returns -1 for what no plan runs. */
+int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* desc, const int32_t* stride, int32_t pass);
+int32_t r3c_conv3d_strided_fwd(const r3c_conv_desc* desc, const int32_t* stride, const void* x, const void* w,
+                               const void* bias, void* y, void* workspace, int64_t workspace_bytes, void* stream);
+int32_t r3c_conv3d_strided_dx(const r3c_conv_desc* desc, const int32_t* stride, const void* dy, const void* w,
+                              void* dx, void* workspace, int64_t workspace_bytes, void* stream);
+int32_t r3c_conv3d_strided_dw(const r3c_conv_desc* desc, const int32_t* stride, const void* x, const void* dy,
+                              void* dw, int32_t dw_dtype, void* db, int32_t db_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
 /* ---- Conv3d over a channel concatenation ------------------------------------
  * No counterpart in the reference package: it replaces the pair
  * torch.cat((a, b), dim=1) + conv3d of the UNet3D decoder (the skip

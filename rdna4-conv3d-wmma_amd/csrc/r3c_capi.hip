@@ -206,7 +206,8 @@ int check_strides(const int64_t* s, const int32_t* dims, const char* what) {
   return R3C_OK;
 }
 
-int validate(const r3c_conv_desc* d, bool transpose) {
+// `st`: Conv3d stride (d, h, w) for the strided entry points; null = 1.
+int validate(const r3c_conv_desc* d, bool transpose, const int32_t* st = nullptr) {
   if (!d) return fail(R3C_INVALID, "descriptor is NULL");
   if (d->dtype != R3C_F16 && d->dtype != R3C_BF16)
     return fail(R3C_UNSUPPORTED, "dtype %d is not fp16 or bf16", d->dtype);
@@ -227,9 +228,14 @@ int validate(const r3c_conv_desc* d, bool transpose) {
     const int k = d->kernel;
     if (d->pad_d < 0 || d->pad_h < 0 || d->pad_w < 0 || d->pad_d > 64 || d->pad_h > 64 || d->pad_w > 64)
       return fail(R3C_UNSUPPORTED, "Conv3d: padding must be in [0, 64]");
-    if (d->od != d->d + 2 * d->pad_d - k + 1 || d->oh != d->h + 2 * d->pad_h - k + 1 ||
-        d->ow != d->w + 2 * d->pad_w - k + 1)
-      return fail(R3C_INVALID, "Conv3d: output dims do not match input + 2*pad - k + 1");
+    const int32_t s1[3] = {1, 1, 1};
+    const int32_t* s = st ? st : s1;
+    for (int i = 0; i < 3; ++i)
+      if (s[i] < 1 || s[i] > 8) return fail(R3C_UNSUPPORTED, "Conv3d: stride %d (only 1 .. 8)", s[i]);
+    const int32_t in[3] = {d->d, d->h, d->w}, pad[3] = {d->pad_d, d->pad_h, d->pad_w}, out[3] = {d->od, d->oh, d->ow};
+    for (int i = 0; i < 3; ++i)
+      if (in[i] + 2 * pad[i] < k || out[i] != (in[i] + 2 * pad[i] - k) / s[i] + 1)
+        return fail(R3C_INVALID, "Conv3d: output dims do not match (input + 2*pad - k) / stride + 1");
   }
   const int32_t xd[5] = {d->n, d->cin, d->d, d->h, d->w};
   const int32_t yd[5] = {d->n, d->cout, d->od, d->oh, d->ow};
@@ -1623,6 +1629,156 @@ int64_t wgrad_ws(const r3c_conv_desc* d, bool transpose) {
   return need;
 }
 
+// ---------------------------------------------------------------------------
+// Conv3d with stride > 1 (r3c_strided.hip)
+// ---------------------------------------------------------------------------
+struct StridedPlan {
+  StridedArgs a;
+  StridedPackArgs pk;
+  int nb;
+  int64_t wpk_bytes;
+};
+
+// Forward (dx false) or dX of a strided Conv3d: wave tiles of 32 destination
+// positions along w (dX: of one residue class of w modulo the stride) and up
+// to 4 column blocks of 32 destination channels.
+void plan_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, StridedPlan& p) {
+  StridedArgs& a = p.a;
+  memset(&a, 0, sizeof a);
+  a.k = d->kernel;
+  a.taps = d->kernel == 3 ? 27 : 1;
+  a.pd = d->pad_d;
+  a.ph = d->pad_h;
+  a.pw = d->pad_w;
+  a.sd = st[0];
+  a.sh = st[1];
+  a.sw = st[2];
+  a.dx = dx ? 1 : 0;
+  const int64_t* ss = dx ? d->y_strides : d->x_strides;
+  const int64_t* sdst = dx ? d->x_strides : d->y_strides;
+  for (int i = 0; i < 5; ++i) {
+    a.ss[i] = ss[i];
+    a.sd5[i] = sdst[i];
+  }
+  a.Cs = dx ? d->cout : d->cin;
+  a.Cd = dx ? d->cin : d->cout;
+  a.Sd = dx ? d->od : d->d;
+  a.Sh = dx ? d->oh : d->h;
+  a.Sw = dx ? d->ow : d->w;
+  a.Rd = dx ? d->d : d->od;
+  a.Rh = dx ? d->h : d->oh;
+  a.Rw = dx ? d->w : d->ow;
+  const int ncb = cdiv(a.Cd, 32);
+  p.nb = std::min(ncb, 4);
+  a.n_ctiles = cdiv(ncb, p.nb);
+  a.nbt = a.n_ctiles * p.nb;
+  a.nc16 = cdiv(a.Cs, 16);
+  a.nwb = dx ? cdiv(cdiv(a.Rw, a.sw), 32) : cdiv(a.Rw, 32);
+  a.ntiles = (int64_t)d->n * a.Rd * a.Rh * (dx ? a.sw : 1) * a.nwb * a.n_ctiles;
+  a.scl = ss[1] == 1 && a.Cs % 8 == 0 && ss[0] % 8 == 0 && ss[2] % 8 == 0 && ss[3] % 8 == 0 && ss[4] % 8 == 0;
+  a.dvec4 = sdst[1] == 1 && a.Cd % 4 == 0 && sdst[0] % 4 == 0 && sdst[2] % 4 == 0 && sdst[3] % 4 == 0 &&
+            sdst[4] % 4 == 0;
+  StridedPackArgs& k = p.pk;
+  memset(&k, 0, sizeof k);
+  k.cin = d->cin;
+  k.cout = d->cout;
+  k.taps = a.taps;
+  k.nbt = a.nbt;
+  k.dx = a.dx;
+  k.total = (int64_t)a.nc16 * a.taps * a.nbt * 64;
+  p.wpk_bytes = align256(k.total * 16);
+}
+
+int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* src, const void* w, const void* bias,
+                void* dst, void* ws, int64_t ws_bytes, void* stream) {
+  int rc = validate(d, false, st);
+  if (rc) return rc;
+  StridedPlan p;
+  plan_strided(d, st, dx, p);
+  if (p.a.ntiles / 4 >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "strided Conv3d: too many output tiles");
+  if (ws_bytes < p.wpk_bytes)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)p.wpk_bytes);
+  if (!src || !w || !dst || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
+  rc = check_device();
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  p.pk.w = static_cast<const uint16_t*>(w);
+  p.pk.out = static_cast<uint16_t*>(ws);
+  {
+    TimedLaunch tl(KIND_PACK, s);
+    launch_strided_pack(p.pk, s);
+    tl.end();
+  }
+  rc = check_launch("strided Conv3d weight pack");
+  if (rc) return rc;
+  StridedArgs& a = p.a;
+  a.src = static_cast<const uint16_t*>(src);
+  a.wpk = static_cast<const uint16_t*>(ws);
+  a.b = dx ? nullptr : static_cast<const uint16_t*>(bias);
+  a.dst = static_cast<uint16_t*>(dst);
+  a.scl = a.scl && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+  a.dvec4 = a.dvec4 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0;
+  TimedLaunch tl(KIND_ROW, s);
+  const bool launched = launch_strided(d->dtype, p.nb, a, s);
+  tl.end();
+  if (!launched) return fail(R3C_UNSUPPORTED, "strided Conv3d: no instantiation for %d column blocks", p.nb);
+  return check_launch(dx ? "strided Conv3d dX" : "strided Conv3d forward");
+}
+
+// The stride-1 convolution whose output grid holds the strided one at
+// multiples of the stride: same input, padding and kernel; dY dense NCDHW.
+void stride1_desc(const r3c_conv_desc* d, r3c_conv_desc& d1) {
+  d1 = *d;
+  d1.od = d->d + 2 * d->pad_d - d->kernel + 1;
+  d1.oh = d->h + 2 * d->pad_h - d->kernel + 1;
+  d1.ow = d->w + 2 * d->pad_w - d->kernel + 1;
+  const int64_t S1 = (int64_t)d1.od * d1.oh * d1.ow;
+  d1.y_strides[0] = (int64_t)d->cout * S1;
+  d1.y_strides[1] = S1;
+  d1.y_strides[2] = (int64_t)d1.oh * d1.ow;
+  d1.y_strides[3] = d1.ow;
+  d1.y_strides[4] = 1;
+}
+
+int64_t dilated_bytes(const r3c_conv_desc& d1) { return align256((int64_t)d1.n * d1.y_strides[0] * 2); }
+
+int run_strided_dw(const r3c_conv_desc* d, const int32_t* st, const void* x, const void* dy, void* dw, int dw_dtype,
+                   void* db, int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
+  int rc = validate(d, false, st);
+  if (rc) return rc;
+  r3c_conv_desc d1;
+  stride1_desc(d, d1);
+  const int64_t dil = dilated_bytes(d1);
+  if (ws_bytes < dil)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)dil);
+  if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
+  rc = check_device();
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  DilateArgs a;
+  memset(&a, 0, sizeof a);
+  a.src = static_cast<const uint16_t*>(dy);
+  a.dst = static_cast<uint16_t*>(ws);
+  for (int i = 0; i < 5; ++i) a.ys[i] = d->y_strides[i];
+  a.C = d->cout;
+  a.D1 = d1.od;
+  a.H1 = d1.oh;
+  a.W1 = d1.ow;
+  a.sd = st[0];
+  a.sh = st[1];
+  a.sw = st[2];
+  a.total = (int64_t)d1.n * d1.y_strides[0];
+  {
+    TimedLaunch tl(KIND_LAYOUT, s);
+    launch_dilate(a, s);
+    tl.end();
+  }
+  rc = check_launch("strided Conv3d dY scatter");
+  if (rc) return rc;
+  return run_wgrad(&d1, false, x, ws, dw, dw_dtype, db, db_dtype, static_cast<char*>(ws) + dil, ws_bytes - dil,
+                   stream);
+}
+
 std::mutex g_dev_mu;
 std::unordered_map<int, int> g_dev_ok;
 
@@ -1706,6 +1862,40 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* d, const void* x, const void* dy, voi
   int rc = validate(d, false);
   if (rc) return rc;
   return run_wgrad(d, false, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
+}
+
+int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* d, const int32_t* stride, int32_t pass) {
+  if (!stride || validate(d, false, stride) != R3C_OK) return -1;
+  if (pass == 0 || pass == 1) {
+    StridedPlan p;
+    plan_strided(d, stride, pass == 1, p);
+    return p.wpk_bytes;
+  }
+  if (pass == 2) {
+    r3c_conv_desc d1;
+    stride1_desc(d, d1);
+    const int64_t inner = wgrad_ws(&d1, false);
+    return inner < 0 ? -1 : dilated_bytes(d1) + inner;
+  }
+  return -1;
+}
+
+int32_t r3c_conv3d_strided_fwd(const r3c_conv_desc* d, const int32_t* stride, const void* x, const void* w,
+                               const void* bias, void* y, void* ws, int64_t ws_bytes, void* stream) {
+  if (!stride) return fail(R3C_INVALID, "stride is NULL");
+  return run_strided(d, stride, false, x, w, bias, y, ws, ws_bytes, stream);
+}
+
+int32_t r3c_conv3d_strided_dx(const r3c_conv_desc* d, const int32_t* stride, const void* dy, const void* w, void* dx,
+                              void* ws, int64_t ws_bytes, void* stream) {
+  if (!stride) return fail(R3C_INVALID, "stride is NULL");
+  return run_strided(d, stride, true, dy, w, nullptr, dx, ws, ws_bytes, stream);
+}
+
+int32_t r3c_conv3d_strided_dw(const r3c_conv_desc* d, const int32_t* stride, const void* x, const void* dy, void* dw,
+                              int32_t dw_dtype, void* db, int32_t db_dtype, void* ws, int64_t ws_bytes, void* stream) {
+  if (!stride) return fail(R3C_INVALID, "stride is NULL");
+  return run_strided_dw(d, stride, x, dy, dw, dw_dtype, db, db_dtype, ws, ws_bytes, stream);
 }
 
 int64_t r3c_conv3d_cat_workspace(const r3c_conv_desc* d, int32_t ca, int64_t xb_sample_stride, int32_t pass) {

@@ -298,6 +298,42 @@ struct StemArgs {
                          //      8 positions per 16-byte store (through LDS)
 };
 
+// Conv3d with stride > 1 (r3c_strided.hip).  Forward: source x, destination
+// y; dX: source dY, destination dX, tiles over residue classes of w.
+struct StridedArgs {
+  const uint16_t* src;
+  const uint16_t* wpk;   // [nc16][taps][nbt][64][8]
+  const uint16_t* b;     // forward bias or null
+  uint16_t* dst;
+  int64_t ss[5];         // source strides (n, c, d, h, w)
+  int64_t sd5[5];        // destination strides
+  int32_t Cs, Cd;        // source (K) channels, destination channels
+  int32_t Sd, Sh, Sw;    // source spatial dims
+  int32_t Rd, Rh, Rw;    // destination spatial dims
+  int32_t k, taps;
+  int32_t pd, ph, pw;    // padding
+  int32_t sd, sh, sw;    // stride
+  int32_t dx;            // 0 forward, 1 dX
+  int32_t nc16, nbt, n_ctiles;
+  int32_t nwb;           // 32-position blocks along w per row (dX: per residue class)
+  int32_t scl;           // 1: source channel-contiguous, 16-byte aligned, Cs % 8 == 0
+  int32_t dvec4;         // 1: destination channel-contiguous, Cd % 4 == 0, 8-byte aligned
+  int64_t ntiles;        // wave tiles
+};
+struct StridedPackArgs {
+  const uint16_t* w;     // OIDHW [cout][cin][taps]
+  uint16_t* out;
+  int32_t cin, cout, taps, nbt, dx;
+  int64_t total;         // fragments (16 bytes each)
+};
+struct DilateArgs {
+  const uint16_t* src;   // strided dY, any strides
+  uint16_t* dst;         // dense NCDHW [n][C][D1][H1][W1]
+  int64_t ys[5];
+  int32_t C, D1, H1, W1, sd, sh, sw;
+  int64_t total;         // elements of dst
+};
+
 struct PoolArgs {
   const void* x;          // forward input
   void* y;                // forward output
@@ -339,6 +375,11 @@ void launch_mfma_probe(int shape, int blocks, int iters, float* out, hipStream_t
 bool launch_skinny(int dtype, int pass, const SkinnyArgs& a, hipStream_t stream);
 // pass 0 = forward, 2 = dW + db; false when Cout has no instantiation.
 bool launch_stem(int dtype, int pass, const StemArgs& a, size_t lds, hipStream_t stream);
+// Strided Conv3d: weight pack, forward / dX kernel (nb column blocks per wave
+// tile, 1..4), and the dY scatter onto the stride-1 grid for dW.
+void launch_strided_pack(const StridedPackArgs& a, hipStream_t stream);
+bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t stream);
+void launch_dilate(const DilateArgs& a, hipStream_t stream);
 void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);
 void launch_maxpool2_bwd(int dtype, const PoolArgs& a, hipStream_t stream);
 

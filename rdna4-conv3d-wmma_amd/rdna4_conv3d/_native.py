@@ -126,6 +126,15 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_conv3d_cat_dx.argtypes = [D, I32, P, P, P, P, ctypes.c_int64, P, ctypes.c_int64, P]
     lib.r3c_conv3d_cat_dw.restype = I32
     lib.r3c_conv3d_cat_dw.argtypes = [D, I32, P, P, ctypes.c_int64, P, P, I32, P, I32, P, ctypes.c_int64, P]
+    S = ctypes.POINTER(I32)
+    lib.r3c_conv3d_strided_workspace.restype = I64
+    lib.r3c_conv3d_strided_workspace.argtypes = [D, S, I32]
+    lib.r3c_conv3d_strided_fwd.restype = I32
+    lib.r3c_conv3d_strided_fwd.argtypes = [D, S, P, P, P, P, P, I64, P]
+    lib.r3c_conv3d_strided_dx.restype = I32
+    lib.r3c_conv3d_strided_dx.argtypes = [D, S, P, P, P, P, I64, P]
+    lib.r3c_conv3d_strided_dw.restype = I32
+    lib.r3c_conv3d_strided_dw.argtypes = [D, S, P, P, P, I32, P, I32, P, I64, P]
     lib.r3c_probe_mfma.restype = I32
     lib.r3c_probe_mfma.argtypes = [I32, I32, I32, P, P]
     Q = ctypes.POINTER(PoolDesc)
@@ -385,6 +394,103 @@ def conv3d_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, padding, dw_dtype
                            _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws), ws.numel(),
                            _stream_handle(x.device))
     _check(lib, rc, "r3c_conv3d_dw")
+    return dw, db
+
+
+# ---------------------------------------------------------------------------
+# Conv3d with stride > 1 (the r3c_conv3d_strided_* entry points)
+# ---------------------------------------------------------------------------
+def _stride3(stride):
+    return (ctypes.c_int32 * 3)(*(int(s) for s in stride))
+
+
+def strided_out_shape(x_shape, weight_shape, stride, padding):
+    n, _, d, h, w = (int(v) for v in x_shape)
+    k = int(weight_shape[2])
+    sp = [(L + 2 * int(p) - k) // int(s) + 1 for L, p, s in zip((d, h, w), padding, stride)]
+    return (n, int(weight_shape[0]), *sp)
+
+
+@lru_cache(maxsize=4096)
+def _strided_plans_ok(x_shape, x_strides, y_shape, y_strides, kernel: int, padding, stride, dtype_code: int) -> bool:
+    lib = load()
+    d = ConvDesc()
+    d.dtype = dtype_code
+    d.n, d.cin, d.d, d.h, d.w = x_shape
+    _, d.cout, d.od, d.oh, d.ow = y_shape
+    d.kernel = kernel
+    d.pad_d, d.pad_h, d.pad_w = padding
+    for i in range(5):
+        d.x_strides[i] = x_strides[i]
+        d.y_strides[i] = y_strides[i]
+    st = _stride3(stride)
+    return all(lib.r3c_conv3d_strided_workspace(ctypes.byref(d), st, p) >= 0 for p in (0, 1, 2))
+
+
+def strided_plans_ok(x: torch.Tensor, weight_shape, stride, padding, dtype: torch.dtype) -> bool:
+    """True when the library has strided forward, dX and dW plans for this
+    convolution (dY in the output's layout, which follows x)."""
+    y_shape = strided_out_shape(x.shape, weight_shape, stride, padding)
+    if min(y_shape[2:]) < 1:
+        return False
+    return _strided_plans_ok(tuple(int(v) for v in x.shape), _passed_strides(x), y_shape,
+                             _dense_strides(y_shape, _out_channels_last(x)), int(weight_shape[2]),
+                             tuple(int(p) for p in padding), tuple(int(s) for s in stride), _DTYPE_CODE[dtype])
+
+
+def conv3d_strided_fwd(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], stride,
+                       padding) -> torch.Tensor:
+    """y = conv3d(x, weight, stride) + bias, k in {1, 3}; y keeps x's layout."""
+    lib = load()
+    x = _dense(x)
+    weight = weight.contiguous()
+    k = int(weight.shape[2])
+    y = _empty_like_layout(strided_out_shape(x.shape, weight.shape, stride, padding), x, x.dtype)
+    desc = make_desc(x.shape, y.shape, k, padding, x.dtype, x.stride(), y.stride())
+    st = _stride3(stride)
+    ws = _workspace(lib.r3c_conv3d_strided_workspace(ctypes.byref(desc), st, 0), x.device, "r3c_conv3d_strided_fwd")
+    b = bias.contiguous() if bias is not None else None
+    rc = lib.r3c_conv3d_strided_fwd(ctypes.byref(desc), st, _ptr(x), _ptr(weight), _ptr(b), _ptr(y), _ptr(ws),
+                                    ws.numel(), _stream_handle(x.device))
+    _check(lib, rc, "r3c_conv3d_strided_fwd")
+    return y
+
+
+def conv3d_strided_dx(go: torch.Tensor, weight: torch.Tensor, x_shape, stride, padding,
+                      like: torch.Tensor) -> torch.Tensor:
+    """dX of a strided Conv3d; dX takes `like`'s memory format."""
+    lib = load()
+    go = _dense(go)
+    weight = weight.contiguous()
+    k = int(weight.shape[2])
+    gx = _empty_like_layout(tuple(int(v) for v in x_shape), like, go.dtype)
+    desc = make_desc(gx.shape, go.shape, k, padding, go.dtype, gx.stride(), go.stride())
+    st = _stride3(stride)
+    ws = _workspace(lib.r3c_conv3d_strided_workspace(ctypes.byref(desc), st, 1), go.device, "r3c_conv3d_strided_dx")
+    rc = lib.r3c_conv3d_strided_dx(ctypes.byref(desc), st, _ptr(go), _ptr(weight), _ptr(gx), _ptr(ws), ws.numel(),
+                                   _stream_handle(go.device))
+    _check(lib, rc, "r3c_conv3d_strided_dx")
+    return gx
+
+
+def conv3d_strided_dw(x: torch.Tensor, go: torch.Tensor, weight_shape, stride, padding, dw_dtype: torch.dtype,
+                      want_db: bool = False, db_dtype: Optional[torch.dtype] = None):
+    """(dW in OIDHW of dw_dtype, db or None) of a strided Conv3d; deterministic."""
+    lib = load()
+    x = _dense(x)
+    go = _dense(go)
+    k = int(weight_shape[2])
+    desc = make_desc(x.shape, go.shape, k, padding, x.dtype, x.stride(), go.stride())
+    st = _stride3(stride)
+    dw = torch.empty(tuple(int(v) for v in weight_shape), device=x.device, dtype=dw_dtype)
+    db = None
+    if want_db:
+        db = torch.empty((int(weight_shape[0]),), device=x.device, dtype=db_dtype or dw_dtype)
+    ws = _workspace(lib.r3c_conv3d_strided_workspace(ctypes.byref(desc), st, 2), x.device, "r3c_conv3d_strided_dw")
+    rc = lib.r3c_conv3d_strided_dw(ctypes.byref(desc), st, _ptr(x), _ptr(go), _ptr(dw), _DTYPE_CODE[dw_dtype],
+                                   _ptr(db), _DTYPE_CODE[db.dtype] if db is not None else R3C_F32, _ptr(ws),
+                                   ws.numel(), _stream_handle(x.device))
+    _check(lib, rc, "r3c_conv3d_strided_dw")
     return dw, db
 
 

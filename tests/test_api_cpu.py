@@ -151,3 +151,22 @@ def test_forward_cat_on_cpu_is_conv_of_cat():
     conv = Conv3dWmma(12, 5, 3, padding=1)
     a, b = torch.randn(2, 8, 4, 5, 6), torch.randn(2, 4, 4, 5, 6)
     torch.testing.assert_close(conv.forward_cat(a, b), conv(torch.cat((a, b), 1)), atol=0, rtol=0)
+
+
+def test_swap_strided_conv3d_and_cpu_fallback():
+    """swap_strided_conv3d replaces exactly the strided nn.Conv3d children
+    (weights, padding_mode kept) and leaves stride-1 ones to swap_conv3d; on
+    the CPU StridedConv3dWmma is nn.Conv3d, bit for bit."""
+    import torch.nn as nn
+    from rdna4_conv3d.strided import StridedConv3dWmma, swap_strided_conv3d
+    torch.manual_seed(0)
+    m = nn.Sequential(nn.Conv3d(2, 4, 3, padding=1), nn.Sequential(nn.Conv3d(4, 8, 3, stride=2, padding=1)),
+                      nn.Conv3d(8, 8, 1, stride=(1, 2, 2), padding_mode="zeros"))
+    x = torch.randn(1, 2, 6, 8, 8)
+    before = m(x)
+    assert swap_strided_conv3d(m) == 2
+    assert type(m[0]) is nn.Conv3d
+    assert type(m[1][0]) is StridedConv3dWmma and type(m[2]) is StridedConv3dWmma
+    assert m[1][0].stride == (2, 2, 2) and m[2].stride == (1, 2, 2)
+    assert torch.equal(m(x), before)
+    assert swap_strided_conv3d(m) == 0

@@ -251,3 +251,29 @@ def test_cat_workspace_query_decides_on_host():
     assert rc == _native.R3C_INVALID
     rc = lib.r3c_conv3d_cat_fwd(ctypes.byref(desc), 20, None, None, 24 * 8 * 16 * 64, None, None, None, None, 0, None)
     assert rc == _native.R3C_UNSUPPORTED
+
+
+def test_strided_workspace_query_validates_on_host():
+    """r3c_conv3d_strided_workspace: output dims (in + 2 pad - k) / stride + 1,
+    strides 1 .. 8, a NULL stride and an unknown pass give -1; each pass of a
+    valid descriptor has a plan (dW: the dY scatter plus the stride-1 dW)."""
+    import torch
+    lib = _native.load()
+    x_shape = (2, 24, 9, 16, 17)
+    y_shape = _native.strided_out_shape(x_shape, (48, 24, 3, 3, 3), (2, 2, 3), (1, 1, 0))
+    assert y_shape == (2, 48, 5, 8, 5)
+    x, y = torch.empty(x_shape), torch.empty(y_shape)
+    d = _native.make_desc(x_shape, y_shape, 3, (1, 1, 0), torch.bfloat16, x.stride(), y.stride())
+    st = _native._stride3((2, 2, 3))
+    sizes = [lib.r3c_conv3d_strided_workspace(ctypes.byref(d), st, p) for p in (0, 1, 2)]
+    assert all(s > 0 for s in sizes), sizes
+    # dW holds the dense dY scatter onto the stride-1 grid (2 x 48 x 7 x 14 x 15 bf16) and more
+    assert sizes[2] >= 2 * 48 * 7 * 14 * 15 * 2
+    assert lib.r3c_conv3d_strided_workspace(ctypes.byref(d), st, 3) == -1
+    assert lib.r3c_conv3d_strided_workspace(ctypes.byref(d), None, 0) == -1
+    for bad in ((2, 2, 2), (0, 2, 3), (9, 2, 3)):   # dims no longer match, or stride out of range
+        assert lib.r3c_conv3d_strided_workspace(ctypes.byref(d), _native._stride3(bad), 0) == -1
+    # stride 1 through the strided entry points is a plain Conv3d descriptor
+    y1 = torch.empty((2, 48, 9, 16, 15))
+    d1 = _native.make_desc(x_shape, y1.shape, 3, (1, 1, 0), torch.bfloat16, x.stride(), y1.stride())
+    assert lib.r3c_conv3d_strided_workspace(ctypes.byref(d1), _native._stride3((1, 1, 1)), 1) > 0
