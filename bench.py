@@ -23,6 +23,9 @@ Also reported on the same JSON line:
                 per-pass time (all kernels of the pass, median of 20, MALL
                 flushed before each by a 512 MB write and a 512 MB read) and
                 compulsory HBM bytes / time vs 8 TB/s.
+  strided_passes  the strided Conv3d (k=3 stride 2, [4,24,64,128,128] -> 48,
+                bf16; outside the reference's stride-1 policy): native and stock
+                (MIOpen) time per pass and TFLOP/s on the algorithmic FLOPs.
   cpu_baseline  the reference's CPU path (Conv3dWmma on CPU tensors ->
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
@@ -358,6 +361,86 @@ def hbm_passes(layout: str, reps: int = 20):
     return out
 
 
+def strided_passes(layout: str, reps: int = 10):
+    """Strided Conv3d (the downsampling convolution, outside the reference's
+    stride-1 policy): k=3 stride 2 pad 1, [4, 24, 64, 128, 128] -> 48 channels
+    bf16.  Native: median of the summed kernel durations of each pass (HIP
+    events on the launch stream, MALL flushed as in hbm_passes).  Stock:
+    F.conv3d / torch.nn.grad on the same tensors, CUDA events around the call.
+    TFLOP/s on the algorithmic 2 N OD OH OW Cout Cin 27."""
+    import torch
+    import torch.nn.functional as F
+    from rdna4_conv3d import _native as nat
+    dev = torch.device("cuda", 0)
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    flush_rd = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def L(t):
+        return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
+
+    def med(v):
+        v = sorted(v)
+        return v[len(v) // 2]
+
+    def native_ms(fn):
+        fn()
+        torch.cuda.synchronize()
+        tot = []
+        for _ in range(reps):
+            flush.zero_()
+            flush_rd.sum()
+            nat.timing_enable(True)
+            nat.timing_collect()
+            fn()
+            recs = nat.timing_collect()
+            nat.timing_enable(False)
+            tot.append(sum(ms for _, _, ms in recs))
+        return med(tot)
+
+    def stock_ms(fn):
+        fn()
+        torch.cuda.synchronize()
+        tot = []
+        for _ in range(reps):
+            flush.zero_()
+            flush_rd.sum()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            tot.append(a.elapsed_time(b))
+        return med(tot)
+
+    n, ci, co, d, h, w, st, pd = 4, 24, 48, 64, 128, 128, (2, 2, 2), (1, 1, 1)
+    x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
+    wt = _kaiming((co, ci, 3, 3, 3), ci * 27, 1, torch.bfloat16).to(dev)
+    b = _kaiming((co,), ci * 27, 3, torch.bfloat16).to(dev)
+    y_shape = nat.strided_out_shape(x.shape, wt.shape, st, pd)
+    go = L(_gen(y_shape, 2, torch.bfloat16).to(dev))
+    flops = 2.0 * n * y_shape[2] * y_shape[3] * y_shape[4] * co * ci * 27
+    native = {
+        "fwd": lambda: nat.conv3d_strided_fwd(x, wt, b, st, pd),
+        "dx": lambda: nat.conv3d_strided_dx(go, wt, x.shape, st, pd, like=x),
+        "dw": lambda: nat.conv3d_strided_dw(x, go, wt.shape, st, pd, torch.float32, want_db=True,
+                                            db_dtype=torch.float32),
+    }
+    stock = {
+        "fwd": lambda: F.conv3d(x, wt, b, st, pd),
+        "dx": lambda: torch.nn.grad.conv3d_input(x.shape, wt, go, st, pd),
+        "dw": lambda: torch.nn.grad.conv3d_weight(x, wt.shape, go, st, pd),
+    }
+    out = {}
+    for p in ("fwd", "dx", "dw"):
+        ms_n, ms_s = native_ms(native[p]), stock_ms(stock[p])
+        out[f"k3s2_{ci}to{co}_{d}x{h}x{w}_bf16_{p}"] = {
+            "us": round(ms_n * 1e3, 2), "tflops": round(flops / (ms_n * 1e-3) / 1e12, 1),
+            "stock_us": round(ms_s * 1e3, 2), "stock_tflops": round(flops / (ms_s * 1e-3) / 1e12, 1)}
+    del x, go, wt, flush, flush_rd
+    torch.cuda.empty_cache()
+    return out
+
+
 def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     """the UNet3D built with this package's layers (and, as
     a second variant, with its fused BatchNorm + ReLU, MaxPool3d(2) and
@@ -680,6 +763,7 @@ def main() -> int:
     del layers
     torch.cuda.empty_cache()
     hbm = None if args.no_hbm_passes else hbm_passes(layout)
+    strided = None if args.no_hbm_passes else strided_passes(layout)
     unet = unet3d_bench(args.unet_steps, 3) if args.unet_steps > 0 else None
     unet32 = unet3d_bench(args.unet_steps, 3, base=32) if args.unet_steps > 0 else None
 
@@ -714,6 +798,7 @@ def main() -> int:
         "roofline": roofline,
         "passes": passes,
         "hbm_passes": hbm,
+        "strided_passes": strided,
         "unet3d": unet,
         "unet3d_base32": unet32,
         "cpu_baseline": cpu,

@@ -1637,6 +1637,7 @@ struct StridedPlan {
   StridedPackArgs pk;
   int nb;
   int64_t wpk_bytes;
+  int64_t copy_bytes;  // > 0: the NCDHW source is first copied to NDHWC (16-byte fragment loads)
 };
 
 // Forward (dx false) or dX of a strided Conv3d: wave tiles of 32 destination
@@ -1687,6 +1688,9 @@ void plan_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, StridedPla
   k.dx = a.dx;
   k.total = (int64_t)a.nc16 * a.taps * a.nbt * 64;
   p.wpk_bytes = align256(k.total * 16);
+  p.copy_bytes = !a.scl && ncdhw_copyable(ss, a.Cs, a.Sd, a.Sh, a.Sw)
+                     ? align256(tensor_bytes(d->n, a.Cs, a.Sd, a.Sh, a.Sw))
+                     : 0;
 }
 
 int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* src, const void* w, const void* bias,
@@ -1696,8 +1700,10 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   StridedPlan p;
   plan_strided(d, st, dx, p);
   if (p.a.ntiles / 4 >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "strided Conv3d: too many output tiles");
-  if (ws_bytes < p.wpk_bytes)
-    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)p.wpk_bytes);
+  if (p.copy_bytes && (reinterpret_cast<uintptr_t>(src) & 15)) p.copy_bytes = 0;  // unaligned: 2-byte loads
+  const int64_t need = p.wpk_bytes + p.copy_bytes;
+  if (ws_bytes < need)
+    return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   if (!src || !w || !dst || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
   rc = check_device();
   if (rc) return rc;
@@ -1713,6 +1719,14 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   if (rc) return rc;
   StridedArgs& a = p.a;
   a.src = static_cast<const uint16_t*>(src);
+  if (p.copy_bytes) {
+    void* cl = static_cast<char*>(ws) + p.wpk_bytes;
+    rc = copy_to_channels_last(src, cl, d->n, a.Cs, a.Sd, a.Sh, a.Sw, s);
+    if (rc) return rc;
+    a.src = static_cast<const uint16_t*>(cl);
+    channels_last_strides(a.ss, a.Cs, a.Sd, a.Sh, a.Sw);
+    a.scl = 1;
+  }
   a.wpk = static_cast<const uint16_t*>(ws);
   a.b = dx ? nullptr : static_cast<const uint16_t*>(bias);
   a.dst = static_cast<uint16_t*>(dst);
@@ -1726,17 +1740,20 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
 }
 
 // The stride-1 convolution whose output grid holds the strided one at
-// multiples of the stride: same input, padding and kernel; dY dense NCDHW.
+// multiples of the stride: same input, padding and kernel; dY NCDHW with rows
+// padded to a multiple of 8 elements.
 void stride1_desc(const r3c_conv_desc* d, r3c_conv_desc& d1) {
   d1 = *d;
   d1.od = d->d + 2 * d->pad_d - d->kernel + 1;
   d1.oh = d->h + 2 * d->pad_h - d->kernel + 1;
   d1.ow = d->w + 2 * d->pad_w - d->kernel + 1;
-  const int64_t S1 = (int64_t)d1.od * d1.oh * d1.ow;
+  // Rows padded to a multiple of 8 elements (16-byte stores of the scatter).
+  const int64_t wp = (d1.ow + 7) / 8 * 8;
+  const int64_t S1 = (int64_t)d1.od * d1.oh * wp;
   d1.y_strides[0] = (int64_t)d->cout * S1;
   d1.y_strides[1] = S1;
-  d1.y_strides[2] = (int64_t)d1.oh * d1.ow;
-  d1.y_strides[3] = d1.ow;
+  d1.y_strides[2] = (int64_t)d1.oh * wp;
+  d1.y_strides[3] = wp;
   d1.y_strides[4] = 1;
 }
 
@@ -1764,10 +1781,11 @@ int run_strided_dw(const r3c_conv_desc* d, const int32_t* st, const void* x, con
   a.D1 = d1.od;
   a.H1 = d1.oh;
   a.W1 = d1.ow;
+  a.W1p = (int32_t)d1.y_strides[3];
   a.sd = st[0];
   a.sh = st[1];
   a.sw = st[2];
-  a.total = (int64_t)d1.n * d1.y_strides[0];
+  a.rows = (int64_t)d1.n * d->cout * d1.od * d1.oh;
   {
     TimedLaunch tl(KIND_LAYOUT, s);
     launch_dilate(a, s);
@@ -1869,7 +1887,7 @@ int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* d, const int32_t* stri
   if (pass == 0 || pass == 1) {
     StridedPlan p;
     plan_strided(d, stride, pass == 1, p);
-    return p.wpk_bytes;
+    return p.wpk_bytes + p.copy_bytes;
   }
   if (pass == 2) {
     r3c_conv_desc d1;

@@ -328,10 +328,10 @@ struct StridedPackArgs {
 };
 struct DilateArgs {
   const uint16_t* src;   // strided dY, any strides
-  uint16_t* dst;         // dense NCDHW [n][C][D1][H1][W1]
+  uint16_t* dst;         // NCDHW [n][C][D1][H1][W1p], 16-byte aligned
   int64_t ys[5];
-  int32_t C, D1, H1, W1, sd, sh, sw;
-  int64_t total;         // elements of dst
+  int32_t C, D1, H1, W1, W1p, sd, sh, sw;  // W1p: row pitch, a multiple of 8 >= W1
+  int64_t rows;          // n * C * D1 * H1
 };
 
 struct PoolArgs {

@@ -58,7 +58,32 @@ __global__ __launch_bounds__(256) void strided_pack_kernel(const StridedPackArgs
   reinterpret_cast<uint4*>(a.out)[v] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
 }
 
-template <typename T, int NB>
+// Tap range of one dimension for a destination coordinate q: taps k0, k0 +
+// step, ... (n of them) with source coordinates c0, c0 + dc, ...  Forward:
+// every tap, source q s - p + k.  dX: the taps with (q + p - k) divisible by
+// s, source (q + p - k) / s.
+struct TapRange {
+  int k0, step, n, c0, dc;
+};
+__device__ __forceinline__ TapRange tap_range(bool dx, int q, int p, int s, int k) {
+  TapRange r;
+  if (!dx) {
+    r.k0 = 0;
+    r.step = 1;
+    r.n = k;
+    r.c0 = q * s - p;
+    r.dc = 1;
+  } else {
+    r.k0 = (q + p) % s;  // q + p >= 0
+    r.step = s;
+    r.n = r.k0 < k ? (k - 1 - r.k0) / s + 1 : 0;
+    r.c0 = (q + p - r.k0) / s;
+    r.dc = -1;
+  }
+  return r;
+}
+
+template <typename T, int NB, int SCL>
 __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -85,54 +110,91 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   const int rw = a.dx ? res + a.sw * j : j;
   const bool pos_ok = rw < a.Rw;
 
+  // Taps that reach the tile, per dimension (uniform; in w the tile's
+  // residue class makes the dX range the same for every lane), and this
+  // lane's source w for the first of them.
+  const TapRange td = tap_range(a.dx, rd, a.pd, a.sd, a.k);
+  const TapRange th = tap_range(a.dx, rh, a.ph, a.sh, a.k);
+  const TapRange tw = tap_range(a.dx, a.dx ? res : rw, a.pw, a.sw, a.k);
+  const int sw0 = a.dx ? j + tw.c0 : tw.c0;
+  const int nc16 = a.nc16;
+  const int total = td.n * th.n * tw.n * nc16;  // K iterations: (tap d, h, w, channel block)
+
   f32x16_t acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[nb][e] = 0.f;
 
-  const uint16_t* src = a.src + (int64_t)n * a.ss[0];
-  const uint4* wpk = reinterpret_cast<const uint4*>(a.wpk);
-  for (int c16 = 0; c16 < a.nc16; ++c16) {
-    const int kch0 = c16 * 16 + 8 * g;  // this lane's 8 source channels
-    const uint16_t* srcc = src + (int64_t)kch0 * a.ss[1];
-    for (int t = 0; t < a.taps; ++t) {
-      const int kd = a.k == 3 ? t / 9 : 0, kh = a.k == 3 ? (t / 3) % 3 : 0, kw = a.k == 3 ? t % 3 : 0;
-      // Source position of this lane for tap t (forward: o*s - p + k; dX:
-      // (i + p - k) / s, which must divide: uniform per tile in d and h, and
-      // in w because the tile holds one residue class).
-      int sd, sh, sw;
-      if (!a.dx) {
-        sd = rd * a.sd - a.pd + kd;
-        sh = rh * a.sh - a.ph + kh;
-        sw = rw * a.sw - a.pw + kw;
-      } else {
-        const int qd = rd + a.pd - kd, qh = rh + a.ph - kh, qw = res + a.pw - kw;
-        if (qd < 0 || qh < 0 || qd % a.sd || qh % a.sh || (qw % a.sw + a.sw) % a.sw) continue;  // uniform
-        sd = qd / a.sd;
-        sh = qh / a.sh;
-        // (res + s j + p - k) / s = j + (qw / s), qw possibly negative but divisible
-        sw = j + (qw >= 0 ? qw / a.sw : -((-qw) / a.sw));
-      }
-      const bool ok = pos_ok && (unsigned)sd < (unsigned)a.Sd && (unsigned)sh < (unsigned)a.Sh &&
-                      (unsigned)sw < (unsigned)a.Sw && kch0 < a.Cs;
-      uint4 bfr = make_uint4(0u, 0u, 0u, 0u);
-      const uint16_t* p = srcc + (int64_t)sd * a.ss[2] + (int64_t)sh * a.ss[3] + (int64_t)sw * a.ss[4];
-      if (a.scl) {
-        if (ok) bfr = *reinterpret_cast<const uint4*>(p);
-      } else {
-        uint32_t wd[4];
+  const uint16_t* src = a.src + (int64_t)n * a.ss[0] + (int64_t)(8 * g) * a.ss[1];
+  const uint4* wpk = reinterpret_cast<const uint4*>(a.wpk) + (int64_t)ct * NB * 64 + lane;
+  // Fragments of K iteration (md, mh, mw, c16), c16 fastest.
+  struct KIt {
+    int c16, mw, mh, md;
+  };
+  // live false: the fragment of a padding iteration (zero source values, so
+  // its MFMAs add nothing; the weight loads stay in range at ki).
+  auto load = [&](const KIt& ki, bool live, uint4& bfr, uint4 (&afr)[NB]) __attribute__((always_inline)) {
+    const int c16 = ki.c16, mw = ki.mw, mh = ki.mh, md = ki.md;
+    const int kd = td.k0 + md * td.step, kh = th.k0 + mh * th.step, kw = tw.k0 + mw * tw.step;
+    // A tile no tap reaches (dX with a large stride) has no live iteration and
+    // taps past the kernel in ki: its weight loads use tap 0.
+    const int t = (live && a.k == 3) ? (kd * 3 + kh) * 3 + kw : 0;
+    const int cd = td.c0 + md * td.dc, ch = th.c0 + mh * th.dc, cw = sw0 + mw * tw.dc;
+    const int kch0 = c16 * 16 + 8 * g;
+    const bool ok = live && pos_ok && (unsigned)cd < (unsigned)a.Sd && (unsigned)ch < (unsigned)a.Sh &&
+                    (unsigned)cw < (unsigned)a.Sw && kch0 < a.Cs;
+    const uint16_t* p =
+        src + (int64_t)(16 * c16) * a.ss[1] + (int64_t)cd * a.ss[2] + (int64_t)ch * a.ss[3] + (int64_t)cw * a.ss[4];
+    if (SCL) {
+      bfr = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      uint32_t wd[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint16_t lo = (ok && kch0 + 2 * q < a.Cs) ? p[(int64_t)(2 * q) * a.ss[1]] : (uint16_t)0;
-          const uint16_t hi = (ok && kch0 + 2 * q + 1 < a.Cs) ? p[(int64_t)(2 * q + 1) * a.ss[1]] : (uint16_t)0;
-          wd[q] = pack2(lo, hi);
-        }
-        bfr = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t lo = (ok && kch0 + 2 * e < a.Cs) ? p[(int64_t)(2 * e) * a.ss[1]] : (uint16_t)0;
+        const uint16_t hi = (ok && kch0 + 2 * e + 1 < a.Cs) ? p[(int64_t)(2 * e + 1) * a.ss[1]] : (uint16_t)0;
+        wd[e] = pack2(lo, hi);
       }
-      const uint4* wrow = wpk + (((int64_t)c16 * a.taps + t) * a.nbt + ct * NB) * 64 + lane;
+      bfr = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    }
+    const uint4* wrow = wpk + ((int64_t)c16 * a.taps + t) * a.nbt * 64;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32<T>(wrow[nb * 64], bfr, acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) afr[nb] = wrow[nb * 64];
+  };
+
+  // Software pipeline, PF iterations deep: slot u holds the fragments of an
+  // iteration it + u; after its MFMAs the slot loads iteration it + u + PF.
+  // The iteration count is padded to a multiple of PF with zero fragments, so
+  // every load is unconditional and each MFMA waits only for its own slot.
+  // The iteration counters advance by carries, no divisions.
+  constexpr int PF = 4;
+  auto advance = [&](KIt& ki) __attribute__((always_inline)) {
+    if (++ki.c16 < nc16) return;
+    ki.c16 = 0;
+    if (++ki.mw < tw.n) return;
+    ki.mw = 0;
+    if (++ki.mh < th.n) return;
+    ki.mh = 0;
+    ++ki.md;
+  };
+  KIt kn = {0, 0, 0, 0};  // next iteration to load (stays at the last one past the end)
+  int loaded = 0;
+  uint4 bq[PF], aq[PF][NB];
+  auto fetch = [&](int u) __attribute__((always_inline)) {
+    const bool live = loaded < total;
+    load(kn, live, bq[u], aq[u]);
+    ++loaded;
+    if (loaded < total) advance(kn);
+  };
+#pragma unroll
+  for (int u = 0; u < PF; ++u) fetch(u);
+  for (int it = 0; it < total; it += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32<T>(aq[u][nb], bq[u], acc[nb]);
+      fetch(u);
     }
   }
 
@@ -164,48 +226,49 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 
 // dY of the strided convolution scattered into the stride-1 output grid
 // (dense NCDHW [n][c][D1][H1][W1]): element (d1, h1, w1) is dy at (d1/s, h1/s,
-// w1/s) when all three divide, else zero.  8 consecutive elements per thread.
+// w1/s) when all three divide, else zero.  Rows have a pitch of W1p (a
+// multiple of 8, the tail past W1 unused); a thread writes 8 consecutive
+// elements of one row as one 16-byte store; rows whose d1 or h1 is not a
+// multiple of the stride are all zeros.
 __global__ __launch_bounds__(256) void dilate_kernel(const DilateArgs a) {
-  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-  if (i0 >= a.total) return;
-  uint16_t v[8];
+  const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int gpr = a.W1p >> 3;  // 8-element groups per row
+  const int64_t row = gi / gpr;
+  if (row >= a.rows) return;
+  const int w0 = (int)(gi - row * gpr) * 8;
+  const int h1 = (int)(row % a.H1);
+  const int64_t r2 = row / a.H1;
+  const int d1 = (int)(r2 % a.D1);
+  const int64_t nc = r2 / a.D1;  // n * C + c
+  uint32_t wd[4] = {0u, 0u, 0u, 0u};
+  if (d1 % a.sd == 0 && h1 % a.sh == 0) {
+    const int c = (int)(nc % a.C);
+    const int64_t n = nc / a.C;
+    const uint16_t* s = a.src + n * a.ys[0] + (int64_t)c * a.ys[1] + (int64_t)(d1 / a.sd) * a.ys[2] +
+                        (int64_t)(h1 / a.sh) * a.ys[3];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t i = i0 + e;
-    v[e] = 0;
-    if (i < a.total) {
-      int64_t r = i;
-      const int w1 = (int)(r % a.W1);
-      r /= a.W1;
-      const int h1 = (int)(r % a.H1);
-      r /= a.H1;
-      const int d1 = (int)(r % a.D1);
-      r /= a.D1;
-      const int c = (int)(r % a.C);
-      const int64_t n = r / a.C;
-      if (d1 % a.sd == 0 && h1 % a.sh == 0 && w1 % a.sw == 0)
-        v[e] = a.src[n * a.ys[0] + c * a.ys[1] + (int64_t)(d1 / a.sd) * a.ys[2] + (int64_t)(h1 / a.sh) * a.ys[3] +
-                     (int64_t)(w1 / a.sw) * a.ys[4]];
+    for (int e = 0; e < 8; ++e) {
+      const int w1 = w0 + e;
+      if (w1 < a.W1 && w1 % a.sw == 0) wd[e >> 1] |= (uint32_t)s[(int64_t)(w1 / a.sw) * a.ys[4]] << (16 * (e & 1));
     }
   }
-  if (i0 + 8 <= a.total) {
-    *reinterpret_cast<uint4*>(a.dst + i0) =
-        make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-  } else {
-    for (int e = 0; e < 8 && i0 + e < a.total; ++e) a.dst[i0 + e] = v[e];
-  }
+  *reinterpret_cast<uint4*>(a.dst + row * a.W1p + w0) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
 }
 
-template <typename T>
-bool launch_t(const StridedArgs& a, int nb, hipStream_t s) {
+template <typename T, int SCL>
+bool launch_ts(const StridedArgs& a, int nb, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.ntiles + 3) / 4);
   switch (nb) {
-    case 1: hipLaunchKernelGGL((strided_kernel<T, 1>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 2: hipLaunchKernelGGL((strided_kernel<T, 2>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 3: hipLaunchKernelGGL((strided_kernel<T, 3>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 4: hipLaunchKernelGGL((strided_kernel<T, 4>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 1: hipLaunchKernelGGL((strided_kernel<T, 1, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((strided_kernel<T, 2, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 3: hipLaunchKernelGGL((strided_kernel<T, 3, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((strided_kernel<T, 4, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
     default: return false;
   }
+}
+template <typename T>
+bool launch_t(const StridedArgs& a, int nb, hipStream_t s) {
+  return a.scl ? launch_ts<T, 1>(a, nb, s) : launch_ts<T, 0>(a, nb, s);
 }
 
 }  // namespace
@@ -219,7 +282,7 @@ bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t s) {
 }
 
 void launch_dilate(const DilateArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(dilate_kernel, dim3((unsigned)((a.total / 8 + 256) / 256)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(dilate_kernel, dim3((unsigned)((a.rows * (a.W1p / 8) + 255) / 256)), dim3(256), 0, s, a);
 }
 
 }  // namespace r3c
