@@ -319,13 +319,16 @@ def _autocast_dtype():
 
 
 def _autocast_args(x, weight, bias):
+    """x in the autocast dtype; weight and bias stay in their parameter dtype.
+    The autograd Functions cast them to the compute dtype for the kernels and
+    return their gradients in that parameter dtype straight from the kernels
+    (fp32 dW / db for fp32 master parameters), so the backward has no cast
+    kernels (autocast's own weight cast would add a bf16 -> fp32 copy per
+    gradient) and dW is not rounded to bf16 on the way."""
     dt = _autocast_dtype()
     if dt is None or not x.is_cuda:
         return x, weight, bias
     x = x.to(dt) if x.dtype != dt else x
-    weight = weight.to(dt) if weight.dtype != dt else weight
-    if bias is not None and bias.dtype != dt:
-        bias = bias.to(dt)
     return x, weight, bias
 
 
@@ -462,9 +465,6 @@ class Conv3dWmma(nn.Conv3d):
         xb = xb.to(xa.dtype) if xb.dtype != xa.dtype else xb
         if xa.dtype not in _HALF:
             return self.forward(torch.cat((xa, xb), 1))
-        w = w.to(xa.dtype) if w.dtype != xa.dtype else w
-        if b is not None and b.dtype != xa.dtype:
-            b = b.to(xa.dtype)
         _ensure_native(xa.device)
         return _Conv3dCatFn.apply(xa, xb, w, b, _t3(self.padding))
 
@@ -486,12 +486,15 @@ class Conv3dWmma(nn.Conv3d):
 
 
 class _Conv3dCatFn(torch.autograd.Function):
-    """k=3 Conv3d over cat(xa, xb) on the native kernels (inputs already in the compute dtype)."""
+    """k=3 Conv3d over cat(xa, xb) on the native kernels (xa, xb in the compute
+    dtype; weight and bias in their parameter dtype, cast here for the kernels)."""
 
     @staticmethod
     def forward(ctx, xa, xb, weight, bias, padding):
+        wc = weight if weight.dtype == xa.dtype else weight.to(xa.dtype)
+        bc = bias if bias is None or bias.dtype == xa.dtype else bias.to(xa.dtype)
         with torch.cuda.device(xa.device):
-            y = _native.conv3d_cat_fwd(xa, xb, weight, bias, padding)
+            y = _native.conv3d_cat_fwd(xa, xb, wc, bc, padding)
         ctx.save_for_backward(xa, xb, weight)
         ctx.padding = padding
         ctx.has_bias = bias is not None
@@ -506,7 +509,8 @@ class _Conv3dCatFn(torch.autograd.Function):
         dxa = dxb = dw = db = None
         with torch.cuda.device(xa.device):
             if need_a or need_b_in:
-                dxa, dxb = _native.conv3d_cat_dx(go, weight, xa.shape, xb.shape, ctx.padding)
+                wc = weight if weight.dtype == xa.dtype else weight.to(xa.dtype)
+                dxa, dxb = _native.conv3d_cat_dx(go, wc, xa.shape, xb.shape, ctx.padding)
             if need_w or (need_bias and ctx.has_bias):
                 dw, db = _native.conv3d_cat_dw(xa, xb, go, weight.shape, ctx.padding, torch.float32,
                                                want_db=need_bias and ctx.has_bias,
