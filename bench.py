@@ -150,7 +150,9 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None, ca
     given, builds the fused BatchNorm + ReLU modules, `pool` the MaxPool3d(2)
     module class (nn.MaxPool3d by default); `cat_free` feeds each decoder
     block's first conv the upsampled tensor and the skip tensor through its
-    forward_cat (no torch.cat) when the conv class has one."""
+    forward_cat (no torch.cat) when the conv class has one, and takes the
+    pooled and skip tensors from the pool's forward_with_skip when it has one
+    (the skip's gradient is added in the pooling backward's pass)."""
     import torch
     import torch.nn as nn
 
@@ -174,8 +176,13 @@ def build_unet3d(conv, tr, base=24, cin=1, classes=2, bnrelu=None, pool=None, ca
             for i, blk in enumerate(self.enc):
                 x = blk(x)
                 if i < 3:
-                    skips.append(x)
-                    x = self.pool(x)
+                    if cat_free and hasattr(self.pool, "forward_with_skip"):
+                        # one backward pass for the pooled path and the skip's gradient
+                        x, skip = self.pool.forward_with_skip(x)
+                        skips.append(skip)
+                    else:
+                        skips.append(x)
+                        x = self.pool(x)
             for up, dec, skip in zip(self.up, self.dec, reversed(skips)):
                 u = up(x)
                 if cat_free and hasattr(dec[0], "forward_cat"):

@@ -261,6 +261,15 @@ int32_t r3c_maxpool2_fwd(const r3c_pool_desc* desc, const void* x, void* y,
                          uint8_t* idx, void* stream);
 int32_t r3c_maxpool2_bwd(const r3c_pool_desc* desc, const void* dy,
                          const uint8_t* idx, void* dx, void* stream);
+/* dx = MaxPool3d backward of dy + add: the UNet3D encoder output feeds both
+ * the pooling and the decoder's skip connection (benches/unet_e2e.py:33-38),
+ * so its gradient is the sum of the two; this writes the sum in the backward's
+ * one pass (no counterpart in the reference, where autograd adds them).  `add`
+ * has x's shape, sample / channel strides add_strides[0..1] (the x_strides
+ * rules) and may be dx itself. */
+int32_t r3c_maxpool2_bwd_add(const r3c_pool_desc* desc, const void* dy,
+                             const uint8_t* idx, const void* add,
+                             const int64_t* add_strides, void* dx, void* stream);
 
 /* ---- MFMA shape probe (measurement only) -------------------------------------
  * No counterpart in the reference.  `blocks` workgroups of 256 threads each

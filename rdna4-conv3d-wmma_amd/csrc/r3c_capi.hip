@@ -2061,13 +2061,24 @@ int32_t r3c_maxpool2_fwd(const r3c_pool_desc* d, const void* x, void* y, uint8_t
   return check_launch("MaxPool3d forward");
 }
 
-int32_t r3c_maxpool2_bwd(const r3c_pool_desc* d, const void* dy, const uint8_t* idx, void* dx, void* stream) {
+static int run_pool_bwd(const r3c_pool_desc* d, const void* dy, const uint8_t* idx, const void* add, const int64_t* add_strides,
+                 void* dx, void* stream) {
   PoolArgs a;
   int rc = pool_setup(d, a);
   if (rc) return rc;
   if (!dy || !idx || !dx) return fail(R3C_INVALID, "NULL pointer");
   if (!aligned16(dx) || (reinterpret_cast<uintptr_t>(dy) & 15) || (reinterpret_cast<uintptr_t>(idx) & 3))
     return fail(R3C_UNSUPPORTED, "MaxPool3d needs 16-byte aligned tensors");
+  if (add) {
+    const int vec = d->dtype == R3C_F32 ? 4 : 8;
+    if (!add_strides || !aligned16(add)) return fail(R3C_UNSUPPORTED, "MaxPool3d: the added gradient must be 16-byte aligned");
+    for (int j = 0; j < 2; ++j)
+      if (add_strides[j] < 0 || add_strides[j] % vec)
+        return fail(R3C_UNSUPPORTED, "MaxPool3d: added gradient strides must be multiples of %d", vec);
+    a.add = add;
+    a.as0 = add_strides[0];
+    a.as1 = add_strides[1];
+  }
   rc = check_device();
   if (rc) return rc;
   a.dy = dy;
@@ -2080,6 +2091,16 @@ int32_t r3c_maxpool2_bwd(const r3c_pool_desc* d, const void* dy, const uint8_t* 
     tl.end();
   }
   return check_launch("MaxPool3d backward");
+}
+
+int32_t r3c_maxpool2_bwd(const r3c_pool_desc* d, const void* dy, const uint8_t* idx, void* dx, void* stream) {
+  return run_pool_bwd(d, dy, idx, nullptr, nullptr, dx, stream);
+}
+
+int32_t r3c_maxpool2_bwd_add(const r3c_pool_desc* d, const void* dy, const uint8_t* idx, const void* add,
+                             const int64_t* add_strides, void* dx, void* stream) {
+  if (!add) return fail(R3C_INVALID, "NULL pointer");
+  return run_pool_bwd(d, dy, idx, add, add_strides, dx, stream);
 }
 
 int32_t r3c_conv3d_dw_static(const r3c_conv_desc* d, const void* x, const void* dy, void* dw, int32_t dw_dtype,

@@ -340,6 +340,8 @@ struct PoolArgs {
   const void* dy;         // backward: gradient of y
   void* dx;               // backward: gradient of x (every element written)
   uint8_t* idx;           // [n][c][od][oh][ow]: kd * 4 + kh * 2 + kw of the window maximum
+  const void* add;        // backward: null, or a tensor shaped like x added to dx (may be dx itself)
+  int64_t as0, as1;       // its sample and channel strides (planes dense)
   int64_t xs0, xs1;       // x / dx sample and channel strides (elements; planes dense)
   int64_t ys0, ys1;       // y / dy sample and channel strides
   int32_t n, c, d, h, w, od, oh, ow;

@@ -9,7 +9,9 @@
 // greater than the running maximum, or NaN, replaces it (so the last NaN
 // wins, and a window of -inf keeps index 0).
 // Backward: every input element receives dy of its window where it is the
-// window's maximum, else 0.
+// window's maximum, else 0; optionally plus the element of a second gradient
+// of x (the skip connection's), added in fp32 and rounded once -- what
+// autograd's sum of the two gradients computes, without a pass of its own.
 //
 // One thread covers 4 consecutive outputs along w: 8 inputs of each of the 4
 // (kd, kh) rows of their windows, as 16-byte vectors (two for fp32).
@@ -153,6 +155,24 @@ __global__ __launch_bounds__(256) void maxpool2_bwd_kernel(const PoolArgs a) {
       for (int kw = 0; kw < 2; ++kw) v[2 * j + kw] = k == r * 2 + kw ? g[j] : 0.f;
     }
     const int64_t o = xb + (int64_t)(r >> 1) * a.h * a.w + (int64_t)(r & 1) * a.w;
+    if (a.add) {  // dx = routed gradient + add, one rounding (as an add of the two tensors)
+      const int64_t ao = (int64_t)p.n * a.as0 + (int64_t)p.c * a.as1 + (o - ((int64_t)p.n * a.xs0 + (int64_t)p.c * a.xs1));
+      if constexpr (DT == DT_F32) {
+        const float* q = static_cast<const float*>(a.add) + ao;
+        const float4 u0 = *reinterpret_cast<const float4*>(q), u1 = *reinterpret_cast<const float4*>(q + 4);
+        v[0] += u0.x; v[1] += u0.y; v[2] += u0.z; v[3] += u0.w;
+        v[4] += u1.x; v[5] += u1.y; v[6] += u1.z; v[7] += u1.w;
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.add) + ao);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint16_t lo = (uint16_t)(qw[e] & 0xffff), hi = (uint16_t)(qw[e] >> 16);
+          v[2 * e] += DT == DT_BF16 ? to_f32<bf16_tag>(lo) : to_f32<f16_tag>(lo);
+          v[2 * e + 1] += DT == DT_BF16 ? to_f32<bf16_tag>(hi) : to_f32<f16_tag>(hi);
+        }
+      }
+    }
     if constexpr (DT == DT_F32) {
       float* d = static_cast<float*>(a.dx) + o;
       *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);

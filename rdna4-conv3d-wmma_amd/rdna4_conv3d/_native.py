@@ -142,6 +142,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.r3c_maxpool2_fwd.argtypes = [Q, P, P, P, P]
     lib.r3c_maxpool2_bwd.restype = I32
     lib.r3c_maxpool2_bwd.argtypes = [Q, P, P, P, P]
+    lib.r3c_maxpool2_bwd_add.restype = I32
+    lib.r3c_maxpool2_bwd_add.argtypes = [Q, P, P, P, ctypes.POINTER(ctypes.c_int64), P, P]
     lib.r3c_conv3d_dw_static.restype = I32
     lib.r3c_conv3d_dw_static.argtypes = [D, P, P, P, I32, P, I32, P]
     lib.r3c_timing_enable.restype = I32
@@ -649,12 +651,18 @@ def maxpool2_fwd(x: torch.Tensor):
     return y, idx
 
 
-def maxpool2_bwd(dy: torch.Tensor, idx: torch.Tensor, x_shape) -> torch.Tensor:
-    """dx of MaxPool3d(2) (NCDHW, every element written)."""
+def maxpool2_bwd(dy: torch.Tensor, idx: torch.Tensor, x_shape, add: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dx of MaxPool3d(2) (NCDHW, every element written), plus `add` (a
+    gradient of x from another consumer, pool_ok layout) when given."""
     lib = load()
     dx = torch.empty(tuple(int(v) for v in x_shape), device=dy.device, dtype=dy.dtype)
     desc = _pool_desc(dx.shape, dx.stride(), dy.stride(), dy.dtype)
-    rc = lib.r3c_maxpool2_bwd(ctypes.byref(desc), _ptr(dy), _ptr(idx), _ptr(dx), _stream_handle(dy.device))
+    if add is None:
+        rc = lib.r3c_maxpool2_bwd(ctypes.byref(desc), _ptr(dy), _ptr(idx), _ptr(dx), _stream_handle(dy.device))
+    else:
+        st = (ctypes.c_int64 * 2)(int(add.stride(0)), int(add.stride(1)))
+        rc = lib.r3c_maxpool2_bwd_add(ctypes.byref(desc), _ptr(dy), _ptr(idx), _ptr(add), st, _ptr(dx),
+                                      _stream_handle(dy.device))
     _check(lib, rc, "r3c_maxpool2_bwd")
     return dx
 

@@ -91,6 +91,37 @@ class _MaxPool2Fn(torch.autograd.Function):
         return _native.maxpool2_bwd(dy, idx, ctx.x_shape)
 
 
+class _MaxPool2SkipFn(torch.autograd.Function):
+    """(MaxPool3d(2)(x), x): a tensor that feeds both the pooling and a skip
+    connection.  The backward receives both gradients and writes their sum in
+    the pooling backward's one pass (r3c_maxpool2_bwd_add) instead of autograd
+    adding them in a pass of its own; the sum is the same (fp32 add, one
+    rounding)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        y, idx = _native.maxpool2_fwd(x)
+        ctx.save_for_backward(idx)
+        ctx.x_shape = tuple(x.shape)
+        return y, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy, dskip):
+        (idx,) = ctx.saved_tensors
+        if dy is None:
+            return dskip
+        dy = dy.contiguous()
+        if dy.data_ptr() % 16:
+            dy = dy.clone()
+        add = None
+        if dskip is not None and dskip.dtype == dy.dtype and dskip.shape == ctx.x_shape and _native.pool_ok(dskip):
+            add = dskip
+        dx = _native.maxpool2_bwd(dy, idx, ctx.x_shape, add=add)
+        if dskip is not None and add is None:
+            dx = dx + dskip
+        return dx
+
+
 def _pair3(v):
     return (v, v, v) if isinstance(v, int) else tuple(v)
 
@@ -115,3 +146,13 @@ class MaxPool3dWmma(nn.MaxPool3d):
         _ensure_native(x.device)
         with torch.cuda.device(x.device):
             return _MaxPool2Fn.apply(x)
+
+    def forward_with_skip(self, x):
+        """(self(x), x) for a tensor that also feeds a skip connection (the
+        UNet3D encoder output): natively, the gradient arriving through the skip
+        is added in the pooling backward's pass.  Elsewhere (x, self(x))."""
+        if not self._native_ok(x):
+            return super().forward(x), x
+        _ensure_native(x.device)
+        with torch.cuda.device(x.device):
+            return _MaxPool2SkipFn.apply(x)

@@ -140,3 +140,38 @@ def test_maxpool_unsupported_shapes_fall_back_to_stock():
         mod = MaxPool3dWmma(2)
         assert not mod._native_ok(x)
         torch.testing.assert_close(mod(x), nn.MaxPool3d(2)(x), atol=0, rtol=0)
+
+
+@requires_gfx950
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "fp16", "fp32"])
+def test_maxpool_forward_with_skip_adds_the_skip_gradient(dtype):
+    """forward_with_skip returns (pool(x), x); the backward writes
+    pool_bwd(dy) + dskip in the pooling's pass (r3c_maxpool2_bwd_add), bitwise
+    what autograd's add of the two gradients gives (fp32 add, one rounding)."""
+    from rdna4_conv3d import _native
+    from rdna4_conv3d.fused import MaxPool3dWmma
+    case = (2, 24, 8, 16, 16)
+    print(f"case MaxPool3dWmma.forward_with_skip {case} {dtype}", flush=True)
+    x = gen(case, 0).to(dtype)
+    go = gen((2, 24, 4, 8, 8), 1).to(dtype)
+    gs = gen(case, 2).to(dtype)
+    y_r, dx_r = _cpu_ref(x, go)
+    want = (dx_r.float() + gs.float()).to(dtype)
+    xg = x.cuda().requires_grad_(True)
+    _native.timing_enable(True)
+    _native.timing_collect()
+    y, skip = MaxPool3dWmma(2).forward_with_skip(xg)
+    torch.autograd.backward([y, skip], [go.cuda(), gs.cuda()])
+    torch.cuda.synchronize()
+    kinds = [k for _, k, _ in _native.timing_collect()]
+    _native.timing_enable(False)
+    assert kinds.count("pool") == 2, kinds  # forward, and one backward pass for both gradients
+    _assert_same(y.detach().cpu(), y_r)
+    assert torch.equal(skip.detach().cpu(), x)
+    _assert_same(xg.grad.cpu(), want)
+    # only one of the two outputs used: the other gradient is absent
+    for use_pool in (True, False):
+        xo = x.cuda().requires_grad_(True)
+        y2, s2 = MaxPool3dWmma(2).forward_with_skip(xo)
+        (y2 if use_pool else s2).backward(go.cuda() if use_pool else gs.cuda())
+        _assert_same(xo.grad.cpu(), dx_r if use_pool else gs)
