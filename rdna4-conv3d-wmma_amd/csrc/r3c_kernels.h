@@ -228,7 +228,7 @@ struct LayoutArgs {
 // BatchNorm3d + ReLU on NCDHW planes (r3c_bn.hip).  Positions of a
 // (sample, channel) plane are contiguous; chunks of kBnChunk positions are the
 // unit of work and of the fixed-order partial sums.
-constexpr int kBnChunk = 16384;
+constexpr int kBnChunk = 8192;
 struct BnArgs {
   const void* y;          // BN input
   const void* dz;         // backward: gradient of the BN + ReLU output

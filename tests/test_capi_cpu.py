@@ -179,7 +179,7 @@ def test_bn_workspace_query_validates_on_host():
 
     ok = bn_desc(4, 24, 64 * 128 * 128, _native.R3C_BF16)
     ws = lib.r3c_bn_relu_workspace(ctypes.byref(ok))
-    nchunk = -(-64 * 128 * 128 // 16384)
+    nchunk = -(-64 * 128 * 128 // 8192)
     assert ws >= 4 * nchunk * 24 * 2 * 4 + 24 * 16
     assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(2, 8, 12, _native.R3C_F32))) > 0      # 12 % 4 == 0
     assert lib.r3c_bn_relu_workspace(ctypes.byref(bn_desc(2, 8, 12, _native.R3C_BF16))) == -1    # 12 % 8 != 0
