@@ -209,8 +209,10 @@ def test_unet3d_loss_tracks_stock():
 @requires_gfx950
 @pytest.mark.timeout(1200)
 @pytest.mark.xfail(strict=False, reason="two correct bf16 computations of this model differ by more than 1e-3 over "
-                   "40 steps (stock NCDHW vs stock channels_last_3d: 2.2e-3 on MI355X); the native layers are the "
-                   "more accurate ones (test_unet3d_layers_at_least_as_accurate_as_stock)")
+                   "40 steps (stock NCDHW vs stock channels_last_3d: 2.2e-3, stock vs stock on the reversed batch: "
+                   "1.85-2.5e-3 on MI355X), so a pass (8.9e-4 measured with fp32 dW of the master weights) is "
+                   "not guaranteed; the native layers are the more accurate ones "
+                   "(test_unet3d_layers_at_least_as_accurate_as_stock)")
 def test_unet3d_north_star_loss_gate():
     c = _curves()
     g = _gap(c["ours"], c["stock"])
