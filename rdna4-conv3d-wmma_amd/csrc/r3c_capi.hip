@@ -1759,10 +1759,113 @@ void stride1_desc(const r3c_conv_desc* d, r3c_conv_desc& d1) {
 
 int64_t dilated_bytes(const r3c_conv_desc& d1) { return align256((int64_t)d1.n * d1.y_strides[0] * 2); }
 
+// Direct strided dW (r3c_strided.hip, strided_dw_kernel): k = 3, w stride 1
+// or 2 with w padding 1, w-contiguous x and dY with 16-byte aligned rows,
+// W % 8 == 0 and OW % 16 == 0 (pointer alignment is the caller's check).
+struct StridedDwPlan {
+  StridedDwArgs a;
+  int sw, ncb;
+  int64_t part_bytes, dbpart_bytes;
+};
+bool plan_strided_dw(const r3c_conv_desc* d, const int32_t* st, StridedDwPlan& p) {
+  const int64_t* xs = d->x_strides;
+  const int64_t* ys = d->y_strides;
+  if (d->kernel != 3 || (st[2] != 1 && st[2] != 2) || d->pad_w != 1 || d->w % 8 || d->ow % 16) return false;
+  if (xs[4] != 1 || xs[3] % 8 || xs[2] % 8 || xs[1] % 8 || xs[0] % 8) return false;
+  if (ys[4] != 1 || ys[3] % 8 || ys[2] % 8 || ys[1] % 8 || ys[0] % 8) return false;
+  StridedDwArgs& a = p.a;
+  memset(&a, 0, sizeof a);
+  a.xs0 = xs[0];
+  a.xs1 = xs[1];
+  a.xs2 = xs[2];
+  a.xs3 = xs[3];
+  a.ys0 = ys[0];
+  a.ys1 = ys[1];
+  a.ys2 = ys[2];
+  a.ys3 = ys[3];
+  a.Cin = d->cin;
+  a.Cout = d->cout;
+  a.D = d->d;
+  a.H = d->h;
+  a.W = d->w;
+  a.OD = d->od;
+  a.OH = d->oh;
+  a.OW = d->ow;
+  a.pd = d->pad_d;
+  a.ph = d->pad_h;
+  a.pw = d->pad_w;
+  a.sd = st[0];
+  a.sh = st[1];
+  p.sw = st[2];
+  p.ncb = d->cout > 32 ? 2 : 1;  // Cout blocks per wave: x fragments serve two MFMAs
+  a.ncg = cdiv(d->cout, 32 * p.ncb);
+  a.ngb = cdiv(d->cin, 32);
+  a.nkb = (int64_t)d->n * d->od * d->oh * (d->ow / 16);
+  // One workgroup (9 waves of 100-152 VGPRs: one fits a CU) per CU, at
+  // least 4 K blocks each, partials within kMaxPartialBytes.
+  const int64_t tiles = (int64_t)a.ncg * a.ngb;
+  const int64_t per_split = (int64_t)d->cout * 27 * d->cin * 4;
+  int64_t ns = std::max<int64_t>(1, kNumCUs / tiles);
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, a.nkb / 4));
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, kMaxPartialBytes / per_split));
+  a.nsplit = (int32_t)ns;
+  p.part_bytes = align256(ns * per_split);
+  p.dbpart_bytes = align256(ns * d->cout * 4);
+  return true;
+}
+
 int run_strided_dw(const r3c_conv_desc* d, const int32_t* st, const void* x, const void* dy, void* dw, int dw_dtype,
                    void* db, int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
   int rc = validate(d, false, st);
   if (rc) return rc;
+  StridedDwPlan dp;
+  if (plan_strided_dw(d, st, dp) && aligned16_all({x, dy})) {
+    const int64_t need = dp.part_bytes + dp.dbpart_bytes;
+    if (ws_bytes < need)
+      return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
+    if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
+    if (dw_dtype != R3C_F32 && dw_dtype != d->dtype) return fail(R3C_INVALID, "dw_dtype must be fp32 or the input dtype");
+    if (db && db_dtype != R3C_F32 && db_dtype != R3C_F16 && db_dtype != R3C_BF16)
+      return fail(R3C_INVALID, "db_dtype must be fp32, fp16 or bf16");
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    StridedDwArgs& a = dp.a;
+    a.x = static_cast<const uint16_t*>(x);
+    a.dy = static_cast<const uint16_t*>(dy);
+    a.part = static_cast<float*>(ws);
+    float* dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + dp.part_bytes);
+    a.dbpart = db ? dbpart : nullptr;
+    {
+      TimedLaunch tl(KIND_WGRAD, s);
+      const bool launched = launch_strided_dw(d->dtype, dp.sw, dp.ncb, a, s);
+      tl.end();
+      if (!launched) return fail(R3C_UNSUPPORTED, "strided dW: no kernel for w stride %d", dp.sw);
+    }
+    rc = check_launch("strided Conv3d dW");
+    if (rc) return rc;
+    ReduceArgs r;
+    memset(&r, 0, sizeof r);
+    r.part = a.part;
+    r.dbpart = dbpart;
+    r.dw = dw;
+    r.db = db;
+    r.nsplit = a.nsplit;
+    r.Fc = d->cout;
+    r.Gc = d->cin;
+    r.taps = 27;
+    r.Fpad = d->cout;
+    r.Gpad = d->cin;
+    r.dw_dtype = dw_dtype;
+    r.db_dtype = db_dtype;
+    r.db_mode = db ? 1 : 0;
+    {
+      TimedLaunch tr(KIND_REDUCE, s);
+      launch_wgrad_reduce(r, s);
+      tr.end();
+    }
+    return check_launch("weight-gradient reduce");
+  }
   r3c_conv_desc d1;
   stride1_desc(d, d1);
   const int64_t dil = dilated_bytes(d1);
@@ -1893,7 +1996,11 @@ int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* d, const int32_t* stri
     r3c_conv_desc d1;
     stride1_desc(d, d1);
     const int64_t inner = wgrad_ws(&d1, false);
-    return inner < 0 ? -1 : dilated_bytes(d1) + inner;
+    if (inner < 0) return -1;
+    int64_t need = dilated_bytes(d1) + inner;
+    StridedDwPlan dp;
+    if (plan_strided_dw(d, stride, dp)) need = std::max(need, dp.part_bytes + dp.dbpart_bytes);
+    return need;
   }
   return -1;
 }

@@ -326,6 +326,22 @@ struct StridedPackArgs {
   int32_t cin, cout, taps, nbt, dx;
   int64_t total;         // fragments (16 bytes each)
 };
+// Direct strided dW (stride along w 1 or 2): workgroup (split, channel-block
+// pair) of 9 waves, wave = (kd, kh) with the 3 kw taps; K blocks of 16 output
+// positions of one row.
+struct StridedDwArgs {
+  const uint16_t* x;     // [n][Cin][D][H][W], w contiguous
+  const uint16_t* dy;    // [n][Cout][OD][OH][OW], ow contiguous
+  float* part;           // [nsplit][Cout][27][Cin]
+  float* dbpart;         // [nsplit][Cout] or null
+  int64_t xs0, xs1, xs2, xs3;   // x strides (n, c, d, h)
+  int64_t ys0, ys1, ys2, ys3;   // dY strides (n, c, d, h)
+  int32_t Cin, Cout, D, H, W, OD, OH, OW;
+  int32_t pd, ph, pw, sd, sh;   // padding; d / h stride (w stride is the template's)
+  int32_t ncg, ngb;      // Cout groups (NCB blocks of 32), Cin blocks of 32; tile = Cout group * ngb + Cin block
+  int64_t nkb;           // K blocks: n * OD * OH * (OW / 16)
+  int32_t nsplit;
+};
 struct DilateArgs {
   const uint16_t* src;   // strided dY, any strides
   uint16_t* dst;         // NCDHW [n][C][D1][H1][W1p], 16-byte aligned
@@ -382,6 +398,8 @@ bool launch_stem(int dtype, int pass, const StemArgs& a, size_t lds, hipStream_t
 void launch_strided_pack(const StridedPackArgs& a, hipStream_t stream);
 bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t stream);
 void launch_dilate(const DilateArgs& a, hipStream_t stream);
+// Direct strided dW + db (sw 1 or 2); false for other w strides.
+bool launch_strided_dw(int dtype, int sw, int ncb, const StridedDwArgs& a, hipStream_t stream);  // ncb: Cout blocks per wave (1, 2)
 void launch_maxpool2_fwd(int dtype, const PoolArgs& a, hipStream_t stream);
 void launch_maxpool2_bwd(int dtype, const PoolArgs& a, hipStream_t stream);
 

@@ -255,6 +255,201 @@ __global__ __launch_bounds__(256) void dilate_kernel(const DilateArgs a) {
   *reinterpret_cast<uint4*>(a.dst + row * a.W1p + w0) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
 }
 
+// Direct strided dW + db: D[co][ci] of tap t summed over output positions.
+// Wave w = (kd, kh) of a workgroup holds the 3 kw taps of one 32 x 32
+// (Cout, Cin) block pair.  K block = 16 output positions (n, od, oh, ow0 ..
+// ow0 + 15) of one row: the dY operand (rows = output channels) is one 16-byte
+// load per lane (positions ow0 + 8 g ..), the x operand (columns = input
+// channels) needs, for kw, input positions SW (ow0 + 8 g + e) - pw + kw: a
+// window of aligned 16-byte loads plus edge dwords around SW (ow0 + 8 g),
+// from which v_alignbit (SW 1) or v_perm (SW 2, every other element) picks
+// the 8 values.  Input rows outside the volume (padding) contribute zeros; the
+// loads of the next PF K blocks are in flight while the current one multiplies.
+// db: wave 0 sums its dY fragments.  One partial per workgroup, added by the
+// fixed-order reduce.  The w padding is 1: with W % 8 == 0 and OW % 16 == 0 it
+// is the only padding a 3-tap window of w stride 1 or 2 allows, and it makes the
+// window picks compile-time register selections.
+template <typename T, int SW, int NCB>
+__global__ __launch_bounds__(576) void strided_dw_kernel(const StridedDwArgs a) {
+  constexpr int NW = SW == 1 ? 6 : 10;  // window dwords: edge, 16 (SW 1) or 32 (SW 2) bytes, edge
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // kd * 3 + kh
+  const int kd = wv / 3, kh = wv % 3;
+  const int g = lane >> 5, li = lane & 31;
+  // Workgroups are dealt to the 8 XCDs in turn; renumber them so that each XCD
+  // runs a contiguous run of (split, tile) pairs, tile fastest: the tiles of a
+  // split and neighbouring splits (which share input planes) share an L2.
+  const int ntile = a.ncg * a.ngb;
+  const int total = a.nsplit * ntile;
+  int bid = blockIdx.x;
+  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int tile = bid % ntile, split = bid / ntile;
+  const int cb = tile / a.ngb, gb = tile % a.ngb;
+  const int64_t k0 = ((int64_t)split * a.nkb) / a.nsplit, k1 = ((int64_t)(split + 1) * a.nkb) / a.nsplit;
+  const int ci = gb * 32 + li;
+  const bool ci_ok = ci < a.Cin;
+  int co[NCB];
+  bool co_ok[NCB];
+#pragma unroll
+  for (int nc = 0; nc < NCB; ++nc) {
+    co[nc] = (cb * NCB + nc) * 32 + li;
+    co_ok[nc] = co[nc] < a.Cout;
+  }
+  const int kpr = a.OW >> 4;  // K blocks per output row
+  f32x16_t acc[NCB][3];
+#pragma unroll
+  for (int nc = 0; nc < NCB; ++nc)
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[nc][k][e] = 0.f;
+  float dbs[NCB];
+#pragma unroll
+  for (int nc = 0; nc < NCB; ++nc) dbs[nc] = 0.f;
+
+  struct Frag {
+    uint4 af[NCB];
+    uint32_t win[NW];
+  };
+  // K block position (n, od, oh, owb), owb fastest; advanced by carries.
+  struct KPos {
+    int owb, oh, od, n;
+  };
+  auto load = [&](const KPos& kp, bool live, Frag& f) __attribute__((always_inline)) {
+    const int ow0 = kp.owb * 16;
+    const uint16_t* yr = a.dy + (int64_t)kp.n * a.ys0 + (int64_t)kp.od * a.ys2 + (int64_t)kp.oh * a.ys3 + ow0 + 8 * g;
+#pragma unroll
+    for (int nc = 0; nc < NCB; ++nc) {
+      f.af[nc] = make_uint4(0u, 0u, 0u, 0u);
+      if (live && co_ok[nc]) f.af[nc] = *reinterpret_cast<const uint4*>(yr + (int64_t)co[nc] * a.ys1);
+    }
+    const int id = kp.od * a.sd - a.pd + kd, ih = kp.oh * a.sh - a.ph + kh;
+    const bool row_ok = live && ci_ok && (unsigned)id < (unsigned)a.D && (unsigned)ih < (unsigned)a.H;
+    const uint16_t* xr =
+        a.x + (int64_t)kp.n * a.xs0 + (int64_t)ci * a.xs1 + (int64_t)id * a.xs2 + (int64_t)ih * a.xs3;
+    const int b = SW * (ow0 + 8 * g);  // first input position of the window's aligned part
+#pragma unroll
+    for (int k = 0; k < NW; ++k) f.win[k] = 0u;
+    if (row_ok) {
+      if (b >= 2) f.win[0] = *reinterpret_cast<const uint32_t*>(xr + b - 2);
+#pragma unroll
+      for (int c = 0; c < SW; ++c)
+        if (b + 8 * c < a.W) {
+          const uint4 m = *reinterpret_cast<const uint4*>(xr + b + 8 * c);
+          f.win[1 + 4 * c] = m.x;
+          f.win[2 + 4 * c] = m.y;
+          f.win[3 + 4 * c] = m.z;
+          f.win[4 + 4 * c] = m.w;
+        }
+      if (b + 8 * SW < a.W) f.win[NW - 1] = *reinterpret_cast<const uint32_t*>(xr + b + 8 * SW);
+    }
+  };
+  auto compute = [&](const Frag& f) __attribute__((always_inline)) {
+    if (wv == 0) {
+#pragma unroll
+      for (int nc = 0; nc < NCB; ++nc) {
+        const uint32_t q[4] = {f.af[nc].x, f.af[nc].y, f.af[nc].z, f.af[nc].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          dbs[nc] += to_f32<T>((uint16_t)(q[e] & 0xffff)) + to_f32<T>((uint16_t)(q[e] >> 16));
+      }
+    }
+#pragma unroll
+    for (int kw = 0; kw < 3; ++kw) {
+      // Window element of value e: j = (kw - pw + 2) + SW e (window element 0 =
+      // input position b - 2).
+      const int o = kw + 1;  // 1 .. 3
+      const int w0 = o >> 1;
+      const bool odd = (o & 1) != 0;
+      uint32_t bw[4];
+      if (SW == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = w0 == 0 ? f.win[q] : (w0 == 1 ? f.win[q + 1] : f.win[q + 2]);
+          const uint32_t hi = w0 == 0 ? f.win[q + 1] : (w0 == 1 ? f.win[q + 2] : (q + 3 < NW ? f.win[q + 3] : 0u));
+          bw[q] = __builtin_amdgcn_alignbit(hi, lo, odd ? 16u : 0u);
+        }
+      } else {
+        const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // values 2q, 2q + 1: window elements o + 4q and o + 4q + 2 (same half)
+          const uint32_t lo = w0 == 0 ? f.win[2 * q] : (w0 == 1 ? f.win[2 * q + 1] : f.win[2 * q + 2]);
+          const uint32_t hi = w0 == 0 ? f.win[2 * q + 1] : (w0 == 1 ? f.win[2 * q + 2] : f.win[2 * q + 3]);
+          bw[q] = __builtin_amdgcn_perm(hi, lo, sel);
+        }
+      }
+      const uint4 bq = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+#pragma unroll
+      for (int nc = 0; nc < NCB; ++nc) acc[nc][kw] = mfma32<T>(f.af[nc], bq, acc[nc][kw]);
+    }
+  };
+
+  // Software pipeline, PF K blocks deep: slot u holds block kb + u and, after
+  // its MFMAs, loads block kb + u + PF.  The count is padded to a multiple of
+  // PF with zero fragments (live false), so each MFMA waits only for its slot.
+  constexpr int PF = NCB == 1 ? 3 : 2;
+  const int nk = (int)(k1 - k0);
+  KPos kn;
+  {
+    int64_t r = k0;
+    kn.owb = (int)(r % kpr);
+    r /= kpr;
+    kn.oh = (int)(r % a.OH);
+    r /= a.OH;
+    kn.od = (int)(r % a.OD);
+    kn.n = (int)(r / a.OD);
+  }
+  auto advance = [&](KPos& kp) __attribute__((always_inline)) {
+    if (++kp.owb < kpr) return;
+    kp.owb = 0;
+    if (++kp.oh < a.OH) return;
+    kp.oh = 0;
+    if (++kp.od < a.OD) return;
+    kp.od = 0;
+    ++kp.n;
+  };
+  int loaded = 0;
+  Frag q[PF];
+  auto fetch = [&](int u) __attribute__((always_inline)) {
+    const bool live = loaded < nk;
+    load(kn, live, q[u]);
+    ++loaded;
+    if (loaded < nk) advance(kn);
+  };
+#pragma unroll
+  for (int u = 0; u < PF; ++u) fetch(u);
+  for (int it = 0; it < nk; it += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      compute(q[u]);
+      fetch(u);
+    }
+  }
+
+  // Partials: acc[nc][kw][4 q + r] = D[co = (cb NCB + nc) 32 + 8 q + 4 g + r][ci = gb 32 + li]
+  // of tap (kd, kh, kw).
+  float* part = a.part + (size_t)split * a.Cout * 27 * a.Cin;
+#pragma unroll
+  for (int nc = 0; nc < NCB; ++nc)
+#pragma unroll
+    for (int kw = 0; kw < 3; ++kw) {
+      const int t = wv * 3 + kw;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int c = (cb * NCB + nc) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+        if (c < a.Cout && ci_ok) part[((size_t)c * 27 + t) * a.Cin + ci] = acc[nc][kw][v];
+      }
+    }
+  if (wv == 0 && gb == 0 && a.dbpart) {
+#pragma unroll
+    for (int nc = 0; nc < NCB; ++nc) {
+      const float tot = dbs[nc] + __shfl_xor(dbs[nc], 32);  // the two position halves of channel co, in a fixed order
+      if (g == 0 && co_ok[nc]) a.dbpart[(size_t)split * a.Cout + co[nc]] = tot;
+    }
+  }
+}
+
 template <typename T, int SCL>
 bool launch_ts(const StridedArgs& a, int nb, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.ntiles + 3) / 4);
@@ -279,6 +474,25 @@ void launch_strided_pack(const StridedPackArgs& a, hipStream_t s) {
 
 bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t s) {
   return dtype == DT_BF16 ? launch_t<bf16_tag>(a, nb, s) : launch_t<f16_tag>(a, nb, s);
+}
+
+template <typename T, int SW>
+void launch_dw_ncb(int ncb, const StridedDwArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.nsplit * a.ncg * a.ngb));
+  if (ncb == 2) hipLaunchKernelGGL((strided_dw_kernel<T, SW, 2>), grid, dim3(576), 0, s, a);
+  else hipLaunchKernelGGL((strided_dw_kernel<T, SW, 1>), grid, dim3(576), 0, s, a);
+}
+
+bool launch_strided_dw(int dtype, int sw, int ncb, const StridedDwArgs& a, hipStream_t s) {
+  if ((sw != 1 && sw != 2) || a.pw != 1 || (ncb != 1 && ncb != 2)) return false;
+  if (dtype == DT_BF16) {
+    if (sw == 1) launch_dw_ncb<bf16_tag, 1>(ncb, a, s);
+    else launch_dw_ncb<bf16_tag, 2>(ncb, a, s);
+  } else {
+    if (sw == 1) launch_dw_ncb<f16_tag, 1>(ncb, a, s);
+    else launch_dw_ncb<f16_tag, 2>(ncb, a, s);
+  }
+  return true;
 }
 
 void launch_dilate(const DilateArgs& a, hipStream_t s) {

@@ -50,7 +50,21 @@ CASES = [
     (2, 20, 3, 5, 6, 9, 1, (0, 0, 1), (2, 1, 2)),        # k = 1
     (1, 8, 130, 4, 5, 12, 3, (1, 1, 1), (2, 2, 2)),      # two column tiles (5 blocks of 32)
     (1, 32, 16, 9, 10, 70, 3, (2, 2, 2), (3, 3, 3)),     # stride 3, w blocks of 32 per residue class
+    # direct dW kernel in NCDHW (w stride 1 or 2, w pad 1, W % 8 == 0, OW % 16 == 0)
+    (2, 24, 48, 8, 32, 32, 3, (1, 1, 1), (2, 2, 2)),     # the downsampling conv, one 16-wide w block
+    (1, 40, 70, 5, 7, 64, 3, (0, 1, 1), (1, 2, 2)),      # ragged channel blocks, d stride 1 pad 0
+    (1, 8, 16, 4, 6, 48, 3, (1, 1, 1), (2, 1, 1)),       # w stride 1: three w blocks per row
+    (2, 16, 32, 16, 32, 64, 3, (1, 1, 1), (2, 2, 2)),    # many K blocks per split
 ]
+
+
+def _direct_dw(case, layout):
+    """Whether the direct strided dW kernel takes this case (else the dY
+    scatter + stride-1 path)."""
+    n, cin, cout, d, h, w, k, pad, stride = case
+    ow = (w + 2 * pad[2] - k) // stride[2] + 1
+    return (layout == "ncdhw" and k == 3 and stride[2] in (1, 2) and pad[2] == 1 and w % 8 == 0
+            and ow % 16 == 0)
 
 
 @requires_gfx950
@@ -75,12 +89,18 @@ def test_strided_native_parity(case, layout, dtype):
     _native.timing_collect()
     y = _native.conv3d_strided_fwd(xg, wg, bg, stride, pad)
     dx = _native.conv3d_strided_dx(gog, wg, xg.shape, stride, pad, like=xg)
+    torch.cuda.synchronize()
+    kinds = [kd for _, kd, _ in _native.timing_collect()]
     dw, db = _native.conv3d_strided_dw(xg, gog, wg.shape, stride, pad, torch.float32, want_db=True,
                                        db_dtype=torch.float32)
     torch.cuda.synchronize()
-    kinds = [kd for _, kd, _ in _native.timing_collect()]
+    dw_kinds = [kd for _, kd, _ in _native.timing_collect()]
     _native.timing_enable(False)
-    assert kinds.count("row") >= 2 and "layout" in kinds and "reduce" in kinds, kinds
+    assert kinds.count("row") >= 2, kinds
+    if _direct_dw(case, layout):
+        assert dw_kinds == ["wgrad", "reduce"], dw_kinds
+    else:
+        assert "layout" in dw_kinds and "reduce" in dw_kinds, dw_kinds
     assert tuple(y.shape) == tuple(y_ref.shape) and dx.shape == dx_ref.shape and dw.shape == dw_ref.shape
     e = [max_rel(y, y_ref), max_rel(dx, dx_ref), max_rel(dw, dw_ref), max_rel(db, db_ref)]
     print("  maxrel y {:.2e} dx {:.2e} dw {:.2e} db {:.2e}".format(*e), flush=True)
