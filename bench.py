@@ -368,6 +368,11 @@ def hbm_passes(layout: str, reps: int = 20):
     return out
 
 
+# The strided pass: the downsampling convolution k=3 stride 2 pad 1,
+# (n, cin, cout, d, h, w, stride, padding).
+STRIDED = (4, 24, 48, 64, 128, 128, (2, 2, 2), (1, 1, 1))
+
+
 def strided_passes(layout: str, reps: int = 10):
     """Strided Conv3d (the downsampling convolution, outside the reference's
     stride-1 policy): k=3 stride 2 pad 1, [4, 24, 64, 128, 128] -> 48 channels
@@ -419,7 +424,7 @@ def strided_passes(layout: str, reps: int = 10):
             tot.append(a.elapsed_time(b))
         return med(tot)
 
-    n, ci, co, d, h, w, st, pd = 4, 24, 48, 64, 128, 128, (2, 2, 2), (1, 1, 1)
+    n, ci, co, d, h, w, st, pd = STRIDED
     x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
     wt = _kaiming((co, ci, 3, 3, 3), ci * 27, 1, torch.bfloat16).to(dev)
     b = _kaiming((co,), ci * 27, 3, torch.bfloat16).to(dev)
@@ -563,7 +568,8 @@ def mfma_probe() -> int:
 def traffic_probe(name: str, layout: str) -> int:
     """Kernels for an HBM-traffic measurement (run under rocprofv3 --pmc): a
     256 MiB device copy three times (FETCH_SIZE / WRITE_SIZE calibration), then
-    the trunk pass `name` (k3_<ci>to<co>_<fwd|dx|dw>) three times."""
+    the trunk pass `name` (k3_<ci>to<co>_<fwd|dx|dw>) or the strided pass
+    (k3s2_24to48_<fwd|dx|dw>, STRIDED) three times."""
     import torch
     from rdna4_conv3d import _native as nat
     dev = torch.device("cuda", 0)
@@ -574,21 +580,31 @@ def traffic_probe(name: str, layout: str) -> int:
     torch.cuda.synchronize()
     del a, b
     stem, p = name.rsplit("_", 1)
-    for (n, ci, co, d, h, w) in TRUNK:
-        if stem == f"k3_{ci}to{co}":
-            break
-    else:
-        print(f"bench.py: unknown probe pass {name}", file=sys.stderr)
-        return 2
+    n, ci, co, d, h, w, st, pd = STRIDED
+    strided = stem == f"k3s2_{ci}to{co}"
+    if not strided:
+        for (n, ci, co, d, h, w) in TRUNK:
+            if stem == f"k3_{ci}to{co}":
+                break
+        else:
+            print(f"bench.py: unknown probe pass {name}", file=sys.stderr)
+            return 2
 
     def L(t):
         return t.contiguous(memory_format=torch.channels_last_3d) if layout == "ndhwc" else t.contiguous()
     x = L(_gen((n, ci, d, h, w), 0, torch.bfloat16).to(dev))
-    go = L(_gen((n, co, d, h, w), 2, torch.bfloat16).to(dev))
     wt = _kaiming((co, ci, 3, 3, 3), ci * 27, 1, torch.bfloat16).to(dev)
     bias = _kaiming((co,), ci * 27, 3, torch.bfloat16).to(dev)
+    y_shape = nat.strided_out_shape(x.shape, wt.shape, st, pd) if strided else (n, co, d, h, w)
+    go = L(_gen(y_shape, 2, torch.bfloat16).to(dev))
     for _ in range(3):
-        if p == "fwd":
+        if strided and p == "fwd":
+            nat.conv3d_strided_fwd(x, wt, bias, st, pd)
+        elif strided and p == "dx":
+            nat.conv3d_strided_dx(go, wt, x.shape, st, pd, like=x)
+        elif strided:
+            nat.conv3d_strided_dw(x, go, wt.shape, st, pd, torch.float32, want_db=True, db_dtype=torch.float32)
+        elif p == "fwd":
             nat.conv3d_fwd(x, wt, bias, (1, 1, 1))
         elif p == "dx":
             nat.conv3d_dx(go, wt, x.shape, (1, 1, 1), like=x)
@@ -611,7 +627,8 @@ def main() -> int:
     ap.add_argument("--no-hbm-passes", action="store_true", help="skip the k=1 / ConvTranspose3d passes")
     ap.add_argument("--probe", default=None, metavar="PASS",
                     help="traffic probe for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB Tensor.copy_ (the "
-                         "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd; or "
+                         "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd, or the "
+                         "strided pass, k3s2_24to48_dw; or "
                          "unet24[_fused|_stock]: 8 UNet3D training steps for a kernel trace; or mfma: "
                          "MFMA shape throughput (32x32x16 vs 16x16x32); exits")
     ap.add_argument("--no-kernel-timing", action="store_true",
