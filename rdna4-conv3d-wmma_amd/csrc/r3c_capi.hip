@@ -1732,6 +1732,8 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   a.dst = static_cast<uint16_t*>(dst);
   a.scl = a.scl && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
   a.dvec4 = a.dvec4 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0;
+  a.dtile = !dx && a.n_ctiles == 1 && a.sd5[1] == 1 && a.sd5[4] == a.Cd && a.Cd % 8 == 0 && a.sd5[0] % 8 == 0 &&
+            a.sd5[2] % 8 == 0 && a.sd5[3] % 8 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
   TimedLaunch tl(KIND_ROW, s);
   const bool launched = launch_strided(d->dtype, p.nb, a, s);
   tl.end();

@@ -88,7 +88,13 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5, li = lane & 31;
-  const int64_t wt = (int64_t)blockIdx.x * 4 + wv;
+  // Workgroups are dealt to the 8 XCDs in turn; renumber them so that each XCD
+  // runs a contiguous run of tiles (neighbouring rows and planes, which read
+  // the same input rows, share an L2).
+  int64_t bid = blockIdx.x;
+  const int64_t nblk = gridDim.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int64_t wt = bid * 4 + wv;
   if (wt >= a.ntiles) return;  // no barrier in this kernel
   // Wave tile -> (column tile, w block, [residue], row, plane, sample).
   int64_t r = wt;
@@ -200,6 +206,36 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 
   // Epilogue: acc[nb][4q + r] = destination channel (ct NB + nb) 32 + 8 q + 4 g + r
   // at this lane's position.
+  if (a.dtile) {
+    // The tile (positions wb 32 .., all Cd channels) is one contiguous run of
+    // the destination: through this wave's LDS block [32 positions][P] and out
+    // as 16-byte chunks, consecutive lanes on consecutive chunks.
+    constexpr int P = 32 * NB + 8;
+    __shared__ __align__(16) uint16_t s_tile[4 * 32 * P];
+    uint16_t* tb = s_tile + wv * (32 * P);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = nb * 32 + 8 * q + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          v[rr] = acc[nb][4 * q + rr] + ((a.b && c0 + rr < a.Cd) ? to_f32<T>(a.b[c0 + rr]) : 0.f);
+        *reinterpret_cast<uint2*>(tb + li * P + c0) =
+            make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])), pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
+      }
+    const int cpp = a.Cd >> 3;  // 16-byte chunks per position
+    const int npos = min(32, a.Rw - wb * 32);
+    uint16_t* dp = a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] +
+                   (int64_t)(wb * 32) * a.Cd;
+    for (int k = lane; k < npos * cpp; k += 64) {
+      const int pos = k / cpp, c8 = k - pos * cpp;
+      *reinterpret_cast<uint4*>(dp + (int64_t)pos * a.Cd + 8 * c8) =
+          *reinterpret_cast<const uint4*>(tb + pos * P + 8 * c8);
+    }
+    return;
+  }
   if (!pos_ok) return;
   uint16_t* dp = a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] + (int64_t)rw * a.sd5[4];
 #pragma unroll
