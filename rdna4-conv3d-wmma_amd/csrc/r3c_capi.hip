@@ -1674,6 +1674,7 @@ void plan_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, StridedPla
   a.n_ctiles = cdiv(ncb, p.nb);
   a.nbt = a.n_ctiles * p.nb;
   a.nc16 = cdiv(a.Cs, 16);
+  a.mb = 1;
   a.nwb = dx ? cdiv(cdiv(a.Rw, a.sw), 32) : cdiv(a.Rw, 32);
   a.ntiles = (int64_t)d->n * a.Rd * a.Rh * (dx ? a.sw : 1) * a.nwb * a.n_ctiles;
   a.scl = ss[1] == 1 && a.Cs % 8 == 0 && ss[0] % 8 == 0 && ss[2] % 8 == 0 && ss[3] % 8 == 0 && ss[4] % 8 == 0;
@@ -1732,6 +1733,19 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   a.dst = static_cast<uint16_t*>(dst);
   a.scl = a.scl && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
   a.dvec4 = a.dvec4 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0;
+  // Two blocks of 32 positions per wave (one weight fragment feeds two MFMAs)
+  // when the fragments are 16-byte loads, at most 2 column blocks (3 waves per
+  // SIMD; more blocks leave 1-2) and at least 8 workgroups per CU remain.
+  {
+    const int64_t per_w = (dx ? cdiv(a.Rw, a.sw) : a.Rw);
+    const int nwb2 = (int)cdiv(per_w, 64);
+    const int64_t nt2 = a.ntiles / a.nwb * nwb2;
+    if (a.scl && p.nb <= 2 && (nt2 + 3) / 4 >= 8ll * kNumCUs) {
+      a.mb = 2;
+      a.nwb = nwb2;
+      a.ntiles = nt2;
+    }
+  }
   a.dtile = !dx && a.n_ctiles == 1 && a.sd5[1] == 1 && a.sd5[4] == a.Cd && a.Cd % 8 == 0 && a.sd5[0] % 8 == 0 &&
             a.sd5[2] % 8 == 0 && a.sd5[3] % 8 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
   TimedLaunch tl(KIND_ROW, s);

@@ -83,7 +83,7 @@ __device__ __forceinline__ TapRange tap_range(bool dx, int q, int p, int s, int 
   return r;
 }
 
-template <typename T, int NB, int SCL>
+template <typename T, int NB, int SCL, int MB>
 __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -111,26 +111,37 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   r /= a.Rh;
   const int rd = (int)(r % a.Rd);
   const int n = (int)(r / a.Rd);
-  // This lane's destination w and whether it exists.
-  const int j = wb * 32 + li;
-  const int rw = a.dx ? res + a.sw * j : j;
-  const bool pos_ok = rw < a.Rw;
+  // This lane's destination w in each of the MB blocks of 32 and whether it
+  // exists.
+  int rw[MB];
+  bool pos_ok[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    const int j = (wb * MB + m) * 32 + li;
+    rw[m] = a.dx ? res + a.sw * j : j;
+    pos_ok[m] = rw[m] < a.Rw;
+  }
 
   // Taps that reach the tile, per dimension (uniform; in w the tile's
   // residue class makes the dX range the same for every lane), and this
   // lane's source w for the first of them.
   const TapRange td = tap_range(a.dx, rd, a.pd, a.sd, a.k);
   const TapRange th = tap_range(a.dx, rh, a.ph, a.sh, a.k);
-  const TapRange tw = tap_range(a.dx, a.dx ? res : rw, a.pw, a.sw, a.k);
-  const int sw0 = a.dx ? j + tw.c0 : tw.c0;
+  const TapRange tw = tap_range(a.dx, a.dx ? res : rw[0], a.pw, a.sw, a.k);  // k0, step, n, dc: lane-free
+  int sw0[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+    sw0[m] = a.dx ? (wb * MB + m) * 32 + li + tw.c0 : rw[m] * a.sw - a.pw;
   const int nc16 = a.nc16;
   const int total = td.n * th.n * tw.n * nc16;  // K iterations: (tap d, h, w, channel block)
 
-  f32x16_t acc[NB];
+  f32x16_t acc[MB][NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
+  for (int m = 0; m < MB; ++m)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[nb][e] = 0.f;
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[m][nb][e] = 0.f;
 
   const uint16_t* src = a.src + (int64_t)n * a.ss[0] + (int64_t)(8 * g) * a.ss[1];
   const uint4* wpk = reinterpret_cast<const uint4*>(a.wpk) + (int64_t)ct * NB * 64 + lane;
@@ -140,29 +151,34 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   };
   // live false: the fragment of a padding iteration (zero source values, so
   // its MFMAs add nothing; the weight loads stay in range at ki).
-  auto load = [&](const KIt& ki, bool live, uint4& bfr, uint4 (&afr)[NB]) __attribute__((always_inline)) {
+  auto load = [&](const KIt& ki, bool live, uint4 (&bfr)[MB], uint4 (&afr)[NB]) __attribute__((always_inline)) {
     const int c16 = ki.c16, mw = ki.mw, mh = ki.mh, md = ki.md;
     const int kd = td.k0 + md * td.step, kh = th.k0 + mh * th.step, kw = tw.k0 + mw * tw.step;
     // A tile no tap reaches (dX with a large stride) has no live iteration and
     // taps past the kernel in ki: its weight loads use tap 0.
     const int t = (live && a.k == 3) ? (kd * 3 + kh) * 3 + kw : 0;
-    const int cd = td.c0 + md * td.dc, ch = th.c0 + mh * th.dc, cw = sw0 + mw * tw.dc;
+    const int cd = td.c0 + md * td.dc, ch = th.c0 + mh * th.dc;
     const int kch0 = c16 * 16 + 8 * g;
-    const bool ok = live && pos_ok && (unsigned)cd < (unsigned)a.Sd && (unsigned)ch < (unsigned)a.Sh &&
-                    (unsigned)cw < (unsigned)a.Sw && kch0 < a.Cs;
-    const uint16_t* p =
-        src + (int64_t)(16 * c16) * a.ss[1] + (int64_t)cd * a.ss[2] + (int64_t)ch * a.ss[3] + (int64_t)cw * a.ss[4];
-    if (SCL) {
-      bfr = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0u, 0u, 0u, 0u);
-    } else {
-      uint32_t wd[4];
+    const bool row_ok =
+        live && (unsigned)cd < (unsigned)a.Sd && (unsigned)ch < (unsigned)a.Sh && kch0 < a.Cs;
+    const uint16_t* prow = src + (int64_t)(16 * c16) * a.ss[1] + (int64_t)cd * a.ss[2] + (int64_t)ch * a.ss[3];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint16_t lo = (ok && kch0 + 2 * e < a.Cs) ? p[(int64_t)(2 * e) * a.ss[1]] : (uint16_t)0;
-        const uint16_t hi = (ok && kch0 + 2 * e + 1 < a.Cs) ? p[(int64_t)(2 * e + 1) * a.ss[1]] : (uint16_t)0;
-        wd[e] = pack2(lo, hi);
+    for (int m = 0; m < MB; ++m) {
+      const int cw = sw0[m] + mw * tw.dc;
+      const bool ok = row_ok && pos_ok[m] && (unsigned)cw < (unsigned)a.Sw;
+      const uint16_t* p = prow + (int64_t)cw * a.ss[4];
+      if (SCL) {
+        bfr[m] = ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0u, 0u, 0u, 0u);
+      } else {
+        uint32_t wd[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint16_t lo = (ok && kch0 + 2 * e < a.Cs) ? p[(int64_t)(2 * e) * a.ss[1]] : (uint16_t)0;
+          const uint16_t hi = (ok && kch0 + 2 * e + 1 < a.Cs) ? p[(int64_t)(2 * e + 1) * a.ss[1]] : (uint16_t)0;
+          wd[e] = pack2(lo, hi);
+        }
+        bfr[m] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
       }
-      bfr = make_uint4(wd[0], wd[1], wd[2], wd[3]);
     }
     const uint4* wrow = wpk + ((int64_t)c16 * a.taps + t) * a.nbt * 64;
 #pragma unroll
@@ -173,7 +189,9 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   // iteration it + u; after its MFMAs the slot loads iteration it + u + PF.
   // The iteration count is padded to a multiple of PF with zero fragments, so
   // every load is unconditional and each MFMA waits only for its own slot.
-  // The iteration counters advance by carries, no divisions.
+  // The iteration counters advance by carries, no divisions.  With MB = 2 a
+  // weight fragment feeds two MFMAs (the vector-memory data path, not the
+  // MFMAs, bounds this kernel).
   constexpr int PF = 4;
   auto advance = [&](KIt& ki) __attribute__((always_inline)) {
     if (++ki.c16 < nc16) return;
@@ -186,7 +204,7 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   };
   KIt kn = {0, 0, 0, 0};  // next iteration to load (stays at the last one past the end)
   int loaded = 0;
-  uint4 bq[PF], aq[PF][NB];
+  uint4 bq[PF][MB], aq[PF][NB];
   auto fetch = [&](int u) __attribute__((always_inline)) {
     const bool live = loaded < total;
     load(kn, live, bq[u], aq[u]);
@@ -199,65 +217,78 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma32<T>(aq[u][nb], bq[u], acc[nb]);
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[m][nb] = mfma32<T>(aq[u][nb], bq[u][m], acc[m][nb]);
       fetch(u);
     }
   }
 
-  // Epilogue: acc[nb][4q + r] = destination channel (ct NB + nb) 32 + 8 q + 4 g + r
-  // at this lane's position.
+  // Epilogue: acc[m][nb][4q + r] = destination channel (ct NB + nb) 32 + 8 q + 4 g + r
+  // at this lane's position of block m.
   if (a.dtile) {
-    // The tile (positions wb 32 .., all Cd channels) is one contiguous run of
+    // Each block of 32 positions (all Cd channels) is one contiguous run of
     // the destination: through this wave's LDS block [32 positions][P] and out
-    // as 16-byte chunks, consecutive lanes on consecutive chunks.
+    // as 16-byte chunks, consecutive lanes on consecutive chunks.  A wave's
+    // LDS operations complete in order, so block m + 1's writes follow block
+    // m's reads.
     constexpr int P = 32 * NB + 8;
     __shared__ __align__(16) uint16_t s_tile[4 * 32 * P];
     uint16_t* tb = s_tile + wv * (32 * P);
+    const int cpp = a.Cd >> 3;  // 16-byte chunks per position
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const int w0 = (wb * MB + m) * 32;
+      if (w0 >= a.Rw) break;  // uniform
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c0 = nb * 32 + 8 * q + 4 * g;
+          float v[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            v[rr] = acc[m][nb][4 * q + rr] + ((a.b && c0 + rr < a.Cd) ? to_f32<T>(a.b[c0 + rr]) : 0.f);
+          *reinterpret_cast<uint2*>(tb + li * P + c0) = make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])),
+                                                                   pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
+        }
+      const int npos = min(32, a.Rw - w0);
+      uint16_t* dp = a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] +
+                     (int64_t)w0 * a.Cd;
+      for (int k = lane; k < npos * cpp; k += 64) {
+        const int pos = k / cpp, c8 = k - pos * cpp;
+        *reinterpret_cast<uint4*>(dp + (int64_t)pos * a.Cd + 8 * c8) =
+            *reinterpret_cast<const uint4*>(tb + pos * P + 8 * c8);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    if (!pos_ok[m]) continue;
+    uint16_t* dp =
+        a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] + (int64_t)rw[m] * a.sd5[4];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int c0 = nb * 32 + 8 * q + 4 * g;
+        const int c0 = (ct * NB + nb) * 32 + 8 * q + 4 * g;
+        if ((ct * NB + nb) * 32 + 8 * q >= a.Cd) break;  // uniform
         float v[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-          v[rr] = acc[nb][4 * q + rr] + ((a.b && c0 + rr < a.Cd) ? to_f32<T>(a.b[c0 + rr]) : 0.f);
-        *reinterpret_cast<uint2*>(tb + li * P + c0) =
-            make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])), pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
+          v[rr] = acc[m][nb][4 * q + rr] + ((a.b && c0 + rr < a.Cd) ? to_f32<T>(a.b[c0 + rr]) : 0.f);
+        if (a.dvec4) {  // channels contiguous, Cd % 4 == 0: one 8-byte store
+          if (c0 < a.Cd)
+            *reinterpret_cast<uint2*>(dp + c0) = make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])),
+                                                            pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
+        } else {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (c0 + rr < a.Cd) dp[(int64_t)(c0 + rr) * a.sd5[1]] = from_f32<T>(v[rr]);
+        }
       }
-    const int cpp = a.Cd >> 3;  // 16-byte chunks per position
-    const int npos = min(32, a.Rw - wb * 32);
-    uint16_t* dp = a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] +
-                   (int64_t)(wb * 32) * a.Cd;
-    for (int k = lane; k < npos * cpp; k += 64) {
-      const int pos = k / cpp, c8 = k - pos * cpp;
-      *reinterpret_cast<uint4*>(dp + (int64_t)pos * a.Cd + 8 * c8) =
-          *reinterpret_cast<const uint4*>(tb + pos * P + 8 * c8);
-    }
-    return;
   }
-  if (!pos_ok) return;
-  uint16_t* dp = a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] + (int64_t)rw * a.sd5[4];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c0 = (ct * NB + nb) * 32 + 8 * q + 4 * g;
-      if ((ct * NB + nb) * 32 + 8 * q >= a.Cd) break;  // uniform
-      float v[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        v[rr] = acc[nb][4 * q + rr] + ((a.b && c0 + rr < a.Cd) ? to_f32<T>(a.b[c0 + rr]) : 0.f);
-      if (a.dvec4) {  // channels contiguous, Cd % 4 == 0: one 8-byte store
-        if (c0 < a.Cd)
-          *reinterpret_cast<uint2*>(dp + c0) =
-              make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])), pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
-      } else {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (c0 + rr < a.Cd) dp[(int64_t)(c0 + rr) * a.sd5[1]] = from_f32<T>(v[rr]);
-      }
-    }
 }
 
 // dY of the strided convolution scattered into the stride-1 output grid
@@ -486,20 +517,21 @@ __global__ __launch_bounds__(576) void strided_dw_kernel(const StridedDwArgs a) 
   }
 }
 
-template <typename T, int SCL>
+template <typename T, int SCL, int MB>
 bool launch_ts(const StridedArgs& a, int nb, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.ntiles + 3) / 4);
   switch (nb) {
-    case 1: hipLaunchKernelGGL((strided_kernel<T, 1, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 2: hipLaunchKernelGGL((strided_kernel<T, 2, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 3: hipLaunchKernelGGL((strided_kernel<T, 3, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
-    case 4: hipLaunchKernelGGL((strided_kernel<T, 4, SCL>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 1: hipLaunchKernelGGL((strided_kernel<T, 1, SCL, MB>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((strided_kernel<T, 2, SCL, MB>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 3: hipLaunchKernelGGL((strided_kernel<T, 3, SCL, MB>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((strided_kernel<T, 4, SCL, MB>), dim3(blocks), dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
 template <typename T>
 bool launch_t(const StridedArgs& a, int nb, hipStream_t s) {
-  return a.scl ? launch_ts<T, 1>(a, nb, s) : launch_ts<T, 0>(a, nb, s);
+  if (a.mb == 2) return a.scl ? launch_ts<T, 1, 2>(a, nb, s) : false;  // two position blocks: 16-byte loads only
+  return a.scl ? launch_ts<T, 1, 1>(a, nb, s) : launch_ts<T, 0, 1>(a, nb, s);
 }
 
 }  // namespace

@@ -155,3 +155,37 @@ def test_strided_module_falls_back_where_not_native():
         mod = StridedConv3dWmma(8, 8, ks, **args).cuda().half()
         assert not strided_native_ok(x, mod.weight, mod.stride, mod.padding, mod.dilation, mod.groups)
         torch.testing.assert_close(mod(x), nn.Conv3d.forward(mod, x), atol=0, rtol=0)
+
+
+@requires_gfx950
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("shape", [(4, 24, 48, 64, 128, 128), (2, 16, 32, 32, 64, 128)],
+                         ids=["bench", "half"])
+def test_strided_native_large_vs_fp32(shape, layout, dtype):
+    """Full-size strided passes (the bench's k=3 stride 2 shape, where the
+    planner gives each wave two blocks of 32 positions, and a half-size one,
+    where dX does) against PyTorch's fp32 convolution of the same rounded
+    values on the GPU; tolerances as above."""
+    from rdna4_conv3d import _native
+    n, cin, cout, d, h, w = shape
+    stride, pad = (2, 2, 2), (1, 1, 1)
+    print(f"case strided large {shape} {layout} {dtype}", flush=True)
+    x = to_layout(gen((n, cin, d, h, w), 0, dtype).cuda(), layout)
+    wt = kaiming_weight((cout, cin, 3, 3, 3), cin * 27, 1, dtype).cuda()
+    b = gen((cout,), 4, dtype).cuda()
+    y_shape = _native.strided_out_shape(x.shape, wt.shape, stride, pad)
+    go = to_layout(gen(y_shape, 2, dtype).cuda(), layout)
+    y = _native.conv3d_strided_fwd(x, wt, b, stride, pad)
+    dx = _native.conv3d_strided_dx(go, wt, x.shape, stride, pad, like=x)
+    dw, db = _native.conv3d_strided_dw(x, go, wt.shape, stride, pad, torch.float32, want_db=True,
+                                       db_dtype=torch.float32)
+    xr = x.detach().float().requires_grad_(True)
+    wr = wt.detach().float().requires_grad_(True)
+    br = b.detach().float().requires_grad_(True)
+    yr = F.conv3d(xr, wr, br, stride, pad)
+    yr.backward(go.float())
+    torch.cuda.synchronize()
+    e = [max_rel(y, yr), max_rel(dx, xr.grad), max_rel(dw, wr.grad), max_rel(db, br.grad)]
+    print("  maxrel y {:.2e} dx {:.2e} dw {:.2e} db {:.2e}".format(*e), flush=True)
+    assert e[0] <= TOL_FWD and e[1] <= TOL_DX and e[2] <= TOL_DW and e[3] <= TOL_DW
