@@ -122,8 +122,10 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
  * kernel 1 or 3, any x / y strides.  Forward and dX: a direct kernel (tiles
  * of one residue class of w for dX); dW + db: a direct kernel for k = 3, w
  * stride 1 or 2, w padding 1, w-contiguous 16-byte aligned rows with W % 8 ==
- * 0 and OW % 16 == 0, else dY scattered onto the stride-1 output grid and the
- * stride-1 weight-gradient kernels (deterministic either way).
+ * 0 and OW % 16 == 0 (dense NDHWC operands with channels and positions
+ * multiples of 8: on NCDHW copies in the workspace), else dY scattered onto
+ * the stride-1 output grid and the stride-1 weight-gradient kernels
+ * (deterministic either way).
  * pass: 0 forward, 1 dX, 2 dW; the query returns -1 for what no plan runs. */
 int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* desc, const int32_t* stride, int32_t pass);
 int32_t r3c_conv3d_strided_fwd(const r3c_conv_desc* desc, const int32_t* stride, const void* x, const void* w,

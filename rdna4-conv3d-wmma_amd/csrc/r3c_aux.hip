@@ -133,6 +133,53 @@ void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(to_channels_last_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
 }
 
+// The inverse copy (NDHWC -> NCDHW), same tiles: each lane loads 8 channels of
+// one position as one 16-byte vector (consecutive lanes on consecutive vectors
+// of the source) and scatters them into LDS [c][p]; then 16-byte stores of 8
+// positions of one channel, lanes along positions.
+__global__ __launch_bounds__(256) void to_channels_first_kernel(const LayoutArgs a) {
+  __shared__ __align__(16) uint16_t tile[32 * kLayoutPitch];
+  const int ncb = (a.C + 31) >> 5;
+  const int64_t ntiles = (a.S + kLayoutTileP - 1) / kLayoutTileP;
+  int64_t b = blockIdx.x;
+  const int64_t pt = b % ntiles;
+  b /= ntiles;
+  const int cb = (int)(b % ncb);
+  const int64_t n = b / ncb;
+  const int c0 = cb * 32;
+  const int cw = a.C - c0 >= 32 ? 32 : a.C - c0;  // channels in this block (multiple of 8)
+  const int64_t p0 = pt * kLayoutTileP;
+  const int np = a.S - p0 >= kLayoutTileP ? kLayoutTileP : (int)(a.S - p0);  // multiple of 8
+  const int tid = threadIdx.x;
+
+  const uint16_t* src = a.src + ((size_t)n * a.S + p0) * a.C + c0;
+  const int cgw = cw >> 3;
+  for (int u = tid; u < np * cgw; u += 256) {
+    const int p = u / cgw, cg = u - (u / cgw) * cgw;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + (size_t)p * a.C + cg * 8);
+    uint16_t* t = tile + cg * 8 * kLayoutPitch + p;
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[(2 * e) * kLayoutPitch] = (uint16_t)(q[e] & 0xffffu);
+      t[(2 * e + 1) * kLayoutPitch] = (uint16_t)(q[e] >> 16);
+    }
+  }
+  __syncthreads();
+  uint16_t* dst = a.dst + ((size_t)n * a.C + c0) * a.S + p0;
+  const int ngrp = np >> 3;
+  for (int it = tid; it < cw * ngrp; it += 256) {
+    const int c = it / ngrp, j = it - (it / ngrp) * ngrp;
+    *reinterpret_cast<uint4*>(dst + (size_t)c * a.S + j * 8) =
+        *reinterpret_cast<const uint4*>(tile + c * kLayoutPitch + j * 8);
+  }
+}
+
+void launch_to_channels_first(const LayoutArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.S + kLayoutTileP - 1) / kLayoutTileP * ((a.C + 31) >> 5) * a.N;
+  hipLaunchKernelGGL(to_channels_first_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+}
+
 template <typename T>
 __device__ __forceinline__ void store_elem(void* base, int64_t i, int dtype, float v) {
   (void)sizeof(T);

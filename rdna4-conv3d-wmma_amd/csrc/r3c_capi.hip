@@ -277,6 +277,23 @@ bool ncdhw_copyable(const int64_t* st, int c, int d, int h, int w) {
          st[0] == (int64_t)c * S;
 }
 
+// Dense NDHWC (channels_last_3d) with C and D H W multiples of 8: the layout
+// the NCDHW copy (to_channels_first_kernel) reads.
+bool ndhwc_copyable(const int64_t* st, int c, int d, int h, int w) {
+  const int64_t S = (int64_t)d * h * w;
+  return c % 8 == 0 && S % 8 == 0 && st[1] == 1 && st[4] == c && st[3] == (int64_t)w * c &&
+         st[2] == (int64_t)h * w * c && st[0] == S * c;
+}
+
+// Element strides (n, c, d, h, w) of the dense NCDHW copy.
+void channels_first_strides(int64_t* st, int c, int d, int h, int w) {
+  st[4] = 1;
+  st[3] = w;
+  st[2] = (int64_t)h * w;
+  st[1] = (int64_t)d * h * w;
+  st[0] = (int64_t)c * d * h * w;
+}
+
 // Element strides (n, c, d, h, w) of the NDHWC copy.
 void channels_last_strides(int64_t* st, int c, int d, int h, int w) {
   st[1] = 1;
@@ -303,6 +320,23 @@ int copy_to_channels_last(const void* src, void* dst, int n, int c, int d, int h
     tl.end();
   }
   return check_launch("layout copy");
+}
+
+int copy_to_channels_first(const void* src, void* dst, int n, int c, int d, int h, int w, hipStream_t s) {
+  if ((reinterpret_cast<uintptr_t>(src) & 15) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15) != 0)
+    return fail(R3C_INVALID, "layout copy needs 16-byte aligned tensors");
+  LayoutArgs la;
+  la.src = static_cast<const uint16_t*>(src);
+  la.dst = static_cast<uint16_t*>(dst);
+  la.S = (int64_t)d * h * w;
+  la.C = c;
+  la.N = n;
+  {
+    TimedLaunch tl(KIND_LAYOUT, s);
+    launch_to_channels_first(la, s);
+    tl.end();
+  }
+  return check_launch("layout copy to NCDHW");
 }
 
 // Bytes of one sample reachable from its base through `strides` (0 if too large
@@ -1830,13 +1864,34 @@ bool plan_strided_dw(const r3c_conv_desc* d, const int32_t* st, StridedDwPlan& p
   return true;
 }
 
+// Dense NDHWC x and dY whose NCDHW copies the direct dW kernel takes: d2 is
+// the descriptor of the copies, xc / yc their workspace bytes.
+bool plan_strided_dw_copies(const r3c_conv_desc* d, const int32_t* st, r3c_conv_desc& d2, StridedDwPlan& p,
+                            int64_t& xc, int64_t& yc) {
+  if (!ndhwc_copyable(d->x_strides, d->cin, d->d, d->h, d->w) ||
+      !ndhwc_copyable(d->y_strides, d->cout, d->od, d->oh, d->ow))
+    return false;
+  d2 = *d;
+  channels_first_strides(d2.x_strides, d->cin, d->d, d->h, d->w);
+  channels_first_strides(d2.y_strides, d->cout, d->od, d->oh, d->ow);
+  if (!plan_strided_dw(&d2, st, p)) return false;
+  xc = align256(tensor_bytes(d->n, d->cin, d->d, d->h, d->w));
+  yc = align256(tensor_bytes(d->n, d->cout, d->od, d->oh, d->ow));
+  return true;
+}
+
 int run_strided_dw(const r3c_conv_desc* d, const int32_t* st, const void* x, const void* dy, void* dw, int dw_dtype,
                    void* db, int db_dtype, void* ws, int64_t ws_bytes, void* stream) {
   int rc = validate(d, false, st);
   if (rc) return rc;
   StridedDwPlan dp;
-  if (plan_strided_dw(d, st, dp) && aligned16_all({x, dy})) {
-    const int64_t need = dp.part_bytes + dp.dbpart_bytes;
+  r3c_conv_desc d2;
+  int64_t xc = 0, yc = 0;
+  const bool aligned = aligned16_all({x, dy});
+  const bool direct = aligned && plan_strided_dw(d, st, dp);
+  const bool copies = aligned && !direct && plan_strided_dw_copies(d, st, d2, dp, xc, yc);
+  if (direct || copies) {
+    const int64_t need = xc + yc + dp.part_bytes + dp.dbpart_bytes;
     if (ws_bytes < need)
       return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
     if (!x || !dy || !dw || !ws) return fail(R3C_INVALID, "NULL tensor pointer");
@@ -1849,8 +1904,18 @@ int run_strided_dw(const r3c_conv_desc* d, const int32_t* st, const void* x, con
     StridedDwArgs& a = dp.a;
     a.x = static_cast<const uint16_t*>(x);
     a.dy = static_cast<const uint16_t*>(dy);
-    a.part = static_cast<float*>(ws);
-    float* dbpart = reinterpret_cast<float*>(static_cast<char*>(ws) + dp.part_bytes);
+    char* wsp = static_cast<char*>(ws);
+    if (copies) {  // NDHWC operands: NCDHW copies in the workspace first
+      rc = copy_to_channels_first(x, wsp, d->n, d->cin, d->d, d->h, d->w, s);
+      if (rc) return rc;
+      rc = copy_to_channels_first(dy, wsp + xc, d->n, d->cout, d->od, d->oh, d->ow, s);
+      if (rc) return rc;
+      a.x = reinterpret_cast<const uint16_t*>(wsp);
+      a.dy = reinterpret_cast<const uint16_t*>(wsp + xc);
+      wsp += xc + yc;
+    }
+    a.part = reinterpret_cast<float*>(wsp);
+    float* dbpart = reinterpret_cast<float*>(wsp + dp.part_bytes);
     a.dbpart = db ? dbpart : nullptr;
     {
       TimedLaunch tl(KIND_WGRAD, s);
@@ -2016,6 +2081,10 @@ int64_t r3c_conv3d_strided_workspace(const r3c_conv_desc* d, const int32_t* stri
     int64_t need = dilated_bytes(d1) + inner;
     StridedDwPlan dp;
     if (plan_strided_dw(d, stride, dp)) need = std::max(need, dp.part_bytes + dp.dbpart_bytes);
+    r3c_conv_desc d2;
+    int64_t xc = 0, yc = 0;
+    if (plan_strided_dw_copies(d, stride, d2, dp, xc, yc))
+      need = std::max(need, xc + yc + dp.part_bytes + dp.dbpart_bytes);
     return need;
   }
   return -1;

@@ -376,6 +376,7 @@ bool launch_row(int dtype, int mode, int nb, int cl, int wf, const RowArgs& a, i
 bool launch_wgrad(int dtype, int mode, int cbw, int cl, int fl, const WgArgs& a, size_t lds_bytes, hipStream_t stream);
 void launch_pack(int dtype, const PackArgs& a, hipStream_t stream);
 void launch_to_channels_last(const LayoutArgs& a, hipStream_t stream);
+void launch_to_channels_first(const LayoutArgs& a, hipStream_t stream);  // NDHWC -> NCDHW
 // One launch: a thread per element (few splits) or a fixed-shape tree over the splits.
 void launch_wgrad_reduce(const ReduceArgs& a, hipStream_t stream);
 // Row-walking k=3 weight gradient (r3c_wgrow.h); false if no instantiation for (gcw, W).

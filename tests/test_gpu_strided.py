@@ -59,12 +59,17 @@ CASES = [
 
 
 def _direct_dw(case, layout):
-    """Whether the direct strided dW kernel takes this case (else the dY
-    scatter + stride-1 path)."""
+    """Which path the strided dW takes: "direct" (the direct kernel on the
+    NCDHW operands), "copies" (NDHWC operands copied to NCDHW, then the direct
+    kernel) or "scatter" (dY scattered onto the stride-1 grid)."""
     n, cin, cout, d, h, w, k, pad, stride = case
-    ow = (w + 2 * pad[2] - k) // stride[2] + 1
-    return (layout == "ncdhw" and k == 3 and stride[2] in (1, 2) and pad[2] == 1 and w % 8 == 0
-            and ow % 16 == 0)
+    od, oh, ow = ((s + 2 * p - k) // st + 1 for s, p, st in zip((d, h, w), pad, stride))
+    if not (k == 3 and stride[2] in (1, 2) and pad[2] == 1 and w % 8 == 0 and ow % 16 == 0):
+        return "scatter"
+    if layout == "ncdhw":
+        return "direct"
+    ok = cin % 8 == 0 and cout % 8 == 0 and (d * h * w) % 8 == 0 and (od * oh * ow) % 8 == 0
+    return "copies" if ok else "scatter"
 
 
 @requires_gfx950
@@ -97,8 +102,11 @@ def test_strided_native_parity(case, layout, dtype):
     dw_kinds = [kd for _, kd, _ in _native.timing_collect()]
     _native.timing_enable(False)
     assert kinds.count("row") >= 2, kinds
-    if _direct_dw(case, layout):
+    path = _direct_dw(case, layout)
+    if path == "direct":
         assert dw_kinds == ["wgrad", "reduce"], dw_kinds
+    elif path == "copies":
+        assert dw_kinds == ["layout", "layout", "wgrad", "reduce"], dw_kinds
     else:
         assert "layout" in dw_kinds and "reduce" in dw_kinds, dw_kinds
     assert tuple(y.shape) == tuple(y_ref.shape) and dx.shape == dx_ref.shape and dw.shape == dw_ref.shape
