@@ -34,7 +34,8 @@ Also reported on the same JSON line:
                 fused BatchNorm + ReLU too, and with stock nn.Conv3d /
                 nn.ConvTranspose3d; the largest loss gaps over 40 steps against
                 stock, and stock's own spread (the batch in reversed order);
-                unet3d_base32 the same at base=32.
+                unet3d_base32 the same at base=32; unet3d_fp16 the same at base=24
+                under fp16 autocast (the reference's protocol).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
 """
@@ -42,6 +43,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -453,11 +455,12 @@ def strided_passes(layout: str, reps: int = 10):
     return out
 
 
-def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
+def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4, amp_dtype=None):
     """the UNet3D built with this package's layers (and, as
     a second variant, with its fused BatchNorm + ReLU, MaxPool3d(2) and
     concatenation-free decoder convs as well) against stock nn.Conv3d /
-    nn.ConvTranspose3d, AMP bf16.
+    nn.ConvTranspose3d, AMP bf16 (amp_dtype torch.float16: the reference's own
+    protocol, torch.autocast("cuda") without a gradient scaler).
 
     Loss tracking is reported against the spread of stock itself: the same
     stock model trained on the same batch with the sample order reversed (a
@@ -471,24 +474,30 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(batch, 1, 64, 128, 128, generator=g).cuda()
     labels = torch.randint(0, 2, (batch, 64, 128, 128), generator=torch.Generator().manual_seed(3)).cuda()
-    ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup)
+    amp = amp_dtype or torch.bfloat16
+    ms_w, loss_w = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup, amp_dtype=amp)
     torch.cuda.empty_cache()
-    ms_f, loss_f = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup,
+    ms_f, loss_f = unet3d_train(Conv3dWmma, ConvTranspose3dWmma, base, x, labels, steps, warmup, amp_dtype=amp,
                                 bnrelu=BatchNormReLU3d, pool=MaxPool3dWmma, cat_free=True)
     torch.cuda.empty_cache()
-    ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup)
+    ms_s, loss_s = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x, labels, steps, warmup, amp_dtype=amp)
     torch.cuda.empty_cache()
     rev = torch.arange(batch - 1, -1, -1, device=x.device)
     _, loss_r = unet3d_train(nn.Conv3d, nn.ConvTranspose3d, base, x[rev].contiguous(), labels[rev].contiguous(),
-                             steps, warmup)
+                             steps, warmup, amp_dtype=amp)
     torch.cuda.empty_cache()
     n40 = min(40, len(loss_s))
 
-    def gap(a, b):
-        return round(max(abs(u - v) for u, v in zip(a[:n40], b[:n40])), 6)
+    def gap(a, b):  # None when a loss is not finite (no NaN in the JSON line)
+        d = [abs(u - v) for u, v in zip(a[:n40], b[:n40])]
+        return round(max(d), 6) if all(math.isfinite(v) for v in d) else None
 
+    def fin(v):
+        return round(v, 6) if math.isfinite(v) else None
+
+    amp_name = "fp16" if amp == torch.float16 else "bf16"
     return {
-        "config": f"base={base} b{batch} x[{batch},1,64,128,128] AMP bf16, CrossEntropy, Adam lr 1e-3, NCDHW",
+        "config": f"base={base} b{batch} x[{batch},1,64,128,128] AMP {amp_name}, CrossEntropy, Adam lr 1e-3, NCDHW",
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms_w, 3),
@@ -504,8 +513,8 @@ def unet3d_bench(steps: int, warmup: int, base: int = 24, batch: int = 4):
         "max_abs_dloss": gap(loss_w, loss_s),
         "max_abs_dloss_all_native": gap(loss_f, loss_s),
         "max_abs_dloss_stock_vs_stock_batch_reversed": gap(loss_r, loss_s),
-        "final_loss": round(loss_w[-1], 6),
-        "stock_final_loss": round(loss_s[-1], 6),
+        "final_loss": fin(loss_w[-1]),
+        "stock_final_loss": fin(loss_s[-1]),
     }
 
 
@@ -790,6 +799,7 @@ def main() -> int:
     strided = None if args.no_hbm_passes else strided_passes(layout)
     unet = unet3d_bench(args.unet_steps, 3) if args.unet_steps > 0 else None
     unet32 = unet3d_bench(args.unet_steps, 3, base=32) if args.unet_steps > 0 else None
+    unet16 = unet3d_bench(args.unet_steps, 3, amp_dtype=torch.float16) if args.unet_steps > 0 else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -825,6 +835,7 @@ def main() -> int:
         "strided_passes": strided,
         "unet3d": unet,
         "unet3d_base32": unet32,
+        "unet3d_fp16": unet16,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
