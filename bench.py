@@ -34,8 +34,8 @@ Also reported on the same JSON line:
                 fused BatchNorm + ReLU too, and with stock nn.Conv3d /
                 nn.ConvTranspose3d; the largest loss gaps over 40 steps against
                 stock, and stock's own spread (the batch in reversed order);
-                unet3d_base32 the same at base=32; unet3d_fp16 the same at base=24
-                under fp16 autocast (the reference's protocol).
+                unet3d_base32 the same at base=32; with --unet-fp16, unet3d_fp16
+                the same at base=24 under fp16 autocast (the reference's protocol).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
 """
@@ -634,6 +634,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--unet-steps", type=int, default=40, help="UNet3D config-5 timed steps (0 skips it)")
     ap.add_argument("--no-hbm-passes", action="store_true", help="skip the k=1 / ConvTranspose3d passes")
+    ap.add_argument("--unet-fp16", action="store_true",
+                    help="also run config 5 under fp16 autocast (the reference's protocol; MIOpen's fp16 kernels "
+                         "are built on first use, which adds minutes on a fresh box)")
     ap.add_argument("--probe", default=None, metavar="PASS",
                     help="traffic probe for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a 256 MiB Tensor.copy_ (the "
                          "calibration) three times, then one trunk pass three times, e.g. k3_24to24_fwd, or the "
@@ -799,7 +802,7 @@ def main() -> int:
     strided = None if args.no_hbm_passes else strided_passes(layout)
     unet = unet3d_bench(args.unet_steps, 3) if args.unet_steps > 0 else None
     unet32 = unet3d_bench(args.unet_steps, 3, base=32) if args.unet_steps > 0 else None
-    unet16 = unet3d_bench(args.unet_steps, 3, amp_dtype=torch.float16) if args.unet_steps > 0 else None
+    unet16 = unet3d_bench(args.unet_steps, 3, amp_dtype=torch.float16) if args.unet_steps > 0 and args.unet_fp16 else None
 
     cpu = None
     if not args.no_cpu_baseline:
