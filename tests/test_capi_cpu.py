@@ -277,3 +277,28 @@ def test_strided_workspace_query_validates_on_host():
     y1 = torch.empty((2, 48, 9, 16, 15))
     d1 = _native.make_desc(x_shape, y1.shape, 3, (1, 1, 0), torch.bfloat16, x.stride(), y1.stride())
     assert lib.r3c_conv3d_strided_workspace(ctypes.byref(d1), _native._stride3((1, 1, 1)), 1) > 0
+
+
+def test_strided_dw_workspace_covers_direct_paths():
+    """The strided dW workspace holds every plan that may run: for a case the
+    direct kernel takes (k=3, w stride 2, w pad 1, W % 8 == 0, OW % 16 == 0) the
+    query covers the 256-split fp32 partials (at most 256 x Cout x 27 x Cin x 4
+    bytes); in NDHWC it also covers the NCDHW copies of x and dY the direct
+    kernel reads there."""
+    import torch
+    lib = _native.load()
+    x_shape = (2, 24, 16, 64, 64)
+    y_shape = _native.strided_out_shape(x_shape, (48, 24, 3, 3, 3), (2, 2, 2), (1, 1, 1))
+    assert y_shape == (2, 48, 8, 32, 32)
+    st = _native._stride3((2, 2, 2))
+    x = torch.empty(x_shape)
+    y = torch.empty(y_shape)
+    d = _native.make_desc(x_shape, y_shape, 3, (1, 1, 1), torch.bfloat16, x.stride(), y.stride())
+    ws = lib.r3c_conv3d_strided_workspace(ctypes.byref(d), st, 2)
+    assert ws >= 48 * 27 * 24 * 4  # at least one split's partials
+    xc = x.contiguous(memory_format=torch.channels_last_3d)
+    yc = y.contiguous(memory_format=torch.channels_last_3d)
+    dc = _native.make_desc(x_shape, y_shape, 3, (1, 1, 1), torch.bfloat16, xc.stride(), yc.stride())
+    wsc = lib.r3c_conv3d_strided_workspace(ctypes.byref(dc), st, 2)
+    copies = (x.numel() + y.numel()) * 2
+    assert wsc >= copies + 48 * 27 * 24 * 4, (wsc, copies)
