@@ -248,6 +248,24 @@ def _rounded_layers():
     return RoundedConv3d, RoundedConvTranspose3d
 
 
+def _gpu_preheat(seconds: float) -> None:
+    """Untimed bf16 matrix products for `seconds`: the GPU's clocks settle
+    within about half a second of sustained load, and a timed loop that
+    starts after host-side work (building a model) would otherwise start
+    below them."""
+    import torch
+    a = torch.ones(4096, 4096, dtype=torch.bfloat16, device="cuda")
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        torch.mm(a, a)
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    del a
+
+
 def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, channels_last=False, bnrelu=None,
                  pool=None, cat_free=False):
     """AMP training of build_unet3d(conv, tr, base) on (x, labels):
@@ -280,6 +298,7 @@ def unet3d_train(conv, tr, base, x, labels, steps, warmup, amp_dtype=None, chann
 
     losses = [step() for _ in range(warmup)]
     torch.cuda.synchronize()
+    _gpu_preheat(0.5)  # clocks at steady state for every variant alike; the model is untouched
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
