@@ -1782,8 +1782,12 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   }
   a.dtile = !dx && a.n_ctiles == 1 && a.sd5[1] == 1 && a.sd5[4] == a.Cd && a.Cd % 8 == 0 && a.sd5[0] % 8 == 0 &&
             a.sd5[2] % 8 == 0 && a.sd5[3] % 8 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+  // Forward with k = 3, w stride 1 or 2, at most 32 source channels and two
+  // column blocks: the x operand through per-wave LDS row segments.
+  const bool rs = !dx && a.k == 3 && a.scl && (a.sw == 1 || a.sw == 2) && a.nc16 <= 2 && p.nb <= 2 &&
+                  (int64_t)a.Sw * a.ss[4] < (1ll << 31);
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = launch_strided(d->dtype, p.nb, a, s);
+  const bool launched = rs ? launch_strided_fwd_rs(d->dtype, p.nb, a, s) : launch_strided(d->dtype, p.nb, a, s);
   tl.end();
   if (!launched) return fail(R3C_UNSUPPORTED, "strided Conv3d: no instantiation for %d column blocks", p.nb);
   return check_launch(dx ? "strided Conv3d dX" : "strided Conv3d forward");
