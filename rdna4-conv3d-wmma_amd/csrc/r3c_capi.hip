@@ -1784,10 +1784,15 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
             a.sd5[2] % 8 == 0 && a.sd5[3] % 8 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
   // Forward with k = 3, w stride 1 or 2, at most 32 source channels and two
   // column blocks: the x operand through per-wave LDS row segments.
-  const bool rs = !dx && a.k == 3 && a.scl && (a.sw == 1 || a.sw == 2) && a.nc16 <= 2 && p.nb <= 2 &&
-                  (int64_t)a.Sw * a.ss[4] < (1ll << 31);
+  // dX likewise with dY row segments (at most 64 dY channels).
+  const bool seg_ok = a.k == 3 && a.scl && (a.sw == 1 || a.sw == 2) && p.nb <= 2 &&
+                      (int64_t)a.Sw * a.ss[4] < (1ll << 31);
+  const bool rs = seg_ok && !dx && a.nc16 <= 2;
+  const bool dxrs = seg_ok && dx && a.nc16 <= 4;
   TimedLaunch tl(KIND_ROW, s);
-  const bool launched = rs ? launch_strided_fwd_rs(d->dtype, p.nb, a, s) : launch_strided(d->dtype, p.nb, a, s);
+  const bool launched = rs     ? launch_strided_fwd_rs(d->dtype, p.nb, a, s)
+                        : dxrs ? launch_strided_dx_rs(d->dtype, p.nb, a, s)
+                               : launch_strided(d->dtype, p.nb, a, s);
   tl.end();
   if (!launched) return fail(R3C_UNSUPPORTED, "strided Conv3d: no instantiation for %d column blocks", p.nb);
   return check_launch(dx ? "strided Conv3d dX" : "strided Conv3d forward");

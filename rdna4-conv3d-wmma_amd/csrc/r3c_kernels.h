@@ -405,6 +405,9 @@ bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t stream)
 // Forward, k = 3, w stride 1 or 2, channel-contiguous source with at most 32 channels, nb <= 2:
 // the x operand through per-wave LDS row segments.
 bool launch_strided_fwd_rs(int dtype, int nb, const StridedArgs& a, hipStream_t stream);
+// dX, k = 3, w stride 1 or 2, channel-contiguous dY with at most 64 channels, nb <= 2: the dY
+// operand through per-wave LDS row segments.
+bool launch_strided_dx_rs(int dtype, int nb, const StridedArgs& a, hipStream_t stream);
 void launch_dilate(const DilateArgs& a, hipStream_t stream);
 // Direct strided dW + db (sw 1 or 2); false for other w strides.
 bool launch_strided_dw(int dtype, int sw, int ncb, const StridedDwArgs& a, hipStream_t stream);  // ncb: Cout blocks per wave (1, 2)

@@ -472,6 +472,158 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
   }
 }
 
+// dX counterpart of strided_fwd_rs_kernel (k = 3, w stride SW 1 or 2, dY
+// channel-contiguous with at most 64 channels): a tile is 32 MB positions of
+// one residue class of w, whose dY positions for tap mw are consecutive
+// (j + c0 - mw), so per (md, mh) the wave loads the dY row segment of
+// 32 MB + tw.n - 1 positions into its LDS block as whole row runs and reads
+// each tap's fragments from there.  Only the taps that reach the tile's
+// residue class are visited (as in strided_kernel); a tile that none reach
+// stores zeros.
+template <typename T, int NB, int MB, int SW, int NC>
+__global__ __launch_bounds__(256, 3) void strided_dx_rs_kernel(const StridedArgs a) {
+  constexpr int SEGMAX = 32 * MB + 2;  // positions of a row segment, at most
+  constexpr int PPS = 2 * NC + 1;
+  constexpr int P = 32 * NB + 8;
+  constexpr int SEGSLOTS = SEGMAX * PPS;
+  constexpr int WSLOTS = SEGSLOTS > 4 * P ? SEGSLOTS : 4 * P;
+  constexpr int NQ = (SEGMAX * 2 * NC + 63) / 64;
+  __shared__ uint4 s_seg[4 * WSLOTS];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5, li = lane & 31;
+  int64_t bid = blockIdx.x;
+  const int64_t nblk = gridDim.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int64_t wt = bid * 4 + wv;
+  if (wt >= a.ntiles) return;  // no barrier in this kernel
+  int64_t r = wt;
+  const int ct = (int)(r % a.n_ctiles);
+  r /= a.n_ctiles;
+  const int wb = (int)(r % a.nwb);
+  r /= a.nwb;
+  const int res = (int)(r % SW);
+  r /= SW;
+  const int rh = (int)(r % a.Rh);
+  r /= a.Rh;
+  const int rd = (int)(r % a.Rd);
+  const int n = (int)(r / a.Rd);
+  const TapRange td = tap_range(true, rd, a.pd, a.sd, 3);
+  const TapRange th = tap_range(true, rh, a.ph, a.sh, 3);
+  const TapRange tw = tap_range(true, res, a.pw, SW, 3);
+  const int j0 = wb * MB * 32;
+  const int seg = 32 * MB + (tw.n > 0 ? tw.n - 1 : 0);  // positions loaded
+  const int s0 = j0 + tw.c0 - (tw.n > 0 ? tw.n - 1 : 0);  // first dY w of the segment
+  uint4* sb = s_seg + wv * WSLOTS;
+
+  const int CG = a.Cs >> 3;
+  for (int q = lane; q < SEGMAX * (2 * NC - CG); q += 64) {
+    const int pos = q / (2 * NC - CG), cg = CG + q % (2 * NC - CG);
+    sb[pos * PPS + cg] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  int goff[NQ], loff[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = lane + 64 * i;
+    const int pos = q / CG, cg = q - (q / CG) * CG;
+    const int cw = s0 + pos;
+    const bool in = q < seg * CG;
+    loff[i] = in ? pos * PPS + cg : -1;
+    goff[i] = (in && (unsigned)cw < (unsigned)a.Sw) ? (int)((int64_t)cw * a.ss[4]) + 8 * cg : -1;
+  }
+  const uint16_t* src = a.src + (int64_t)n * a.ss[0];
+  const int nst = td.n * th.n;
+  uint4 pf[NQ];
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int md = st / (th.n > 0 ? th.n : 1), mh = st - md * (th.n > 0 ? th.n : 1);
+    const int cd = td.c0 + md * td.dc, ch = th.c0 + mh * th.dc;
+    const bool row_ok = st < nst && (unsigned)cd < (unsigned)a.Sd && (unsigned)ch < (unsigned)a.Sh;
+    const uint16_t* rowp = src + (int64_t)cd * a.ss[2] + (int64_t)ch * a.ss[3];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      pf[i] = (row_ok && goff[i] >= 0) ? *reinterpret_cast<const uint4*>(rowp + goff[i]) : make_uint4(0u, 0u, 0u, 0u);
+  };
+  auto commit = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      if (loff[i] >= 0) sb[loff[i]] = pf[i];
+  };
+
+  f32x16_t acc[MB][NB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[m][nb][e] = 0.f;
+  const uint4* wpk = reinterpret_cast<const uint4*>(a.wpk) + (int64_t)ct * NB * 64 + lane;
+
+  if (nst > 0 && tw.n > 0) {
+    issue(0);
+    commit();
+    issue(1);
+    for (int st = 0; st < nst; ++st) {
+      __asm__ volatile("" ::: "memory");  // the segment's LDS writes stay ahead of its reads
+      const int md = st / th.n, mh = st - md * th.n;
+      const int kd = td.k0 + md * td.step, kh = th.k0 + mh * th.step;
+      for (int mw = 0; mw < tw.n; ++mw) {  // uniform, at most 3
+        const int kw = tw.k0 + mw * tw.step;
+        const int t = (kd * 3 + kh) * 3 + kw;
+        uint4 wf[NC][NB];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) wf[c][nb] = wpk[((int64_t)(c * a.taps + t) * a.nbt + nb) * 64];
+        const int pb = tw.n - 1 - mw;  // segment position of this tap's first lane, block 0
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          uint4 bf[MB];
+#pragma unroll
+          for (int m = 0; m < MB; ++m) bf[m] = sb[(m * 32 + li + pb) * PPS + 2 * c + g];
+#pragma unroll
+          for (int m = 0; m < MB; ++m)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) acc[m][nb] = mfma32<T>(wf[c][nb], bf[m], acc[m][nb]);
+        }
+      }
+      __asm__ volatile("" ::: "memory");  // this segment's LDS reads are issued before the next one's writes
+      if (st + 1 < nst) {
+        commit();
+        if (st + 2 < nst) issue(st + 2);
+      }
+    }
+  }
+
+  // Epilogue: acc[m][nb][4q + r] = destination channel (ct NB + nb) 32 + 8 q + 4 g + r at
+  // w = res + SW (j0 + 32 m + li).
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    const int rw = res + SW * (j0 + 32 * m + li);
+    if (rw >= a.Rw) continue;
+    uint16_t* dp =
+        a.dst + (int64_t)n * a.sd5[0] + (int64_t)rd * a.sd5[2] + (int64_t)rh * a.sd5[3] + (int64_t)rw * a.sd5[4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = (ct * NB + nb) * 32 + 8 * q + 4 * g;
+        if ((ct * NB + nb) * 32 + 8 * q >= a.Cd) break;  // uniform
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) v[rr] = acc[m][nb][4 * q + rr];
+        if (a.dvec4) {
+          if (c0 < a.Cd)
+            *reinterpret_cast<uint2*>(dp + c0) = make_uint2(pack2(from_f32<T>(v[0]), from_f32<T>(v[1])),
+                                                            pack2(from_f32<T>(v[2]), from_f32<T>(v[3])));
+        } else {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (c0 + rr < a.Cd) dp[(int64_t)(c0 + rr) * a.sd5[1]] = from_f32<T>(v[rr]);
+        }
+      }
+  }
+}
+
 // dY of the strided convolution scattered into the stride-1 output grid
 // (dense NCDHW [n][c][D1][H1][W1]): element (d1, h1, w1) is dy at (d1/s, h1/s,
 // w1/s) when all three divide, else zero.  Rows have a pitch of W1p (a
@@ -732,6 +884,29 @@ bool launch_rs_t(const StridedArgs& a, int nb, hipStream_t s) {
   return false;
 }
 
+template <typename T, int NB, int MB, int SW>
+bool launch_dxrs_nc(const StridedArgs& a, unsigned blocks, hipStream_t s) {
+  switch (a.nc16) {
+    case 1: hipLaunchKernelGGL((strided_dx_rs_kernel<T, NB, MB, SW, 1>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((strided_dx_rs_kernel<T, NB, MB, SW, 2>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 3: hipLaunchKernelGGL((strided_dx_rs_kernel<T, NB, MB, SW, 3>), dim3(blocks), dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((strided_dx_rs_kernel<T, NB, MB, SW, 4>), dim3(blocks), dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+template <typename T, int NB, int MB>
+bool launch_dxrs_sw(const StridedArgs& a, unsigned blocks, hipStream_t s) {
+  return a.sw == 1 ? launch_dxrs_nc<T, NB, MB, 1>(a, blocks, s)
+                   : (a.sw == 2 ? launch_dxrs_nc<T, NB, MB, 2>(a, blocks, s) : false);
+}
+template <typename T>
+bool launch_dxrs_t(const StridedArgs& a, int nb, hipStream_t s) {
+  const unsigned blocks = (unsigned)((a.ntiles + 3) / 4);
+  if (nb == 1) return a.mb == 2 ? launch_dxrs_sw<T, 1, 2>(a, blocks, s) : launch_dxrs_sw<T, 1, 1>(a, blocks, s);
+  if (nb == 2) return a.mb == 2 ? launch_dxrs_sw<T, 2, 2>(a, blocks, s) : launch_dxrs_sw<T, 2, 1>(a, blocks, s);
+  return false;
+}
+
 }  // namespace
 
 void launch_strided_pack(const StridedPackArgs& a, hipStream_t s) {
@@ -740,6 +915,10 @@ void launch_strided_pack(const StridedPackArgs& a, hipStream_t s) {
 
 bool launch_strided_fwd_rs(int dtype, int nb, const StridedArgs& a, hipStream_t s) {
   return dtype == DT_BF16 ? launch_rs_t<bf16_tag>(a, nb, s) : launch_rs_t<f16_tag>(a, nb, s);
+}
+
+bool launch_strided_dx_rs(int dtype, int nb, const StridedArgs& a, hipStream_t s) {
+  return dtype == DT_BF16 ? launch_dxrs_t<bf16_tag>(a, nb, s) : launch_dxrs_t<f16_tag>(a, nb, s);
 }
 
 bool launch_strided(int dtype, int nb, const StridedArgs& a, hipStream_t s) {

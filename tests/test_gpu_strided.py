@@ -55,6 +55,9 @@ CASES = [
     (1, 40, 70, 5, 7, 64, 3, (0, 1, 1), (1, 2, 2)),      # ragged channel blocks, d stride 1 pad 0
     (1, 8, 16, 4, 6, 48, 3, (1, 1, 1), (2, 1, 1)),       # w stride 1: three w blocks per row
     (2, 16, 32, 16, 32, 64, 3, (1, 1, 1), (2, 2, 2)),    # many K blocks per split
+    # dX through LDS dY row segments with two column blocks (Cin 33-64)
+    (1, 40, 32, 6, 10, 32, 3, (1, 1, 1), (2, 2, 2)),
+    (1, 48, 24, 5, 6, 16, 3, (1, 1, 1), (1, 1, 1)),      # stride 1 through the strided entry points
 ]
 
 
