@@ -1,0 +1,172 @@
+"""Index math of the strided kernels that stage source rows through LDS
+(csrc/r3c_strided.hip: strided_fwd_rs_kernel, strided_dx_rs_kernel),
+replayed on the CPU with numpy and checked against PyTorch's float64
+convolution, with every LDS slot and every source element the replay touches
+asserted inside its buffer.
+
+Per wave tile the replay follows the kernel step by step: the per-lane chunk
+table (position, 8-channel group) of a row segment, the zero-filled K-padding
+slots, the LDS slot of each chunk (pitch 2 NC + 1 slots per position), the
+segment position each (block, lane, tap) fragment read uses, and the taps of
+one residue class of w for dX (tap_range).  A plausible slip -- a wrong
+segment origin, tap order, residue class or pitch -- changes the result or
+trips a bounds assertion.
+"""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+
+def tap_range(dx: bool, q: int, p: int, s: int, k: int = 3):
+    """(k0, step, n, c0, dc) as the kernels' tap_range."""
+    if not dx:
+        return 0, 1, k, q * s - p, 1
+    k0 = (q + p) % s
+    n = (k - 1 - k0) // s + 1 if k0 < k else 0
+    return k0, s, n, (q + p - k0) // s, -1
+
+
+def run_segment_tile(lds, wslots, src, n, row, s0, seg, segmax, nc, cs, sw_len):
+    """One row segment into the wave's LDS block, as issue() + commit(): chunk
+    q of the segment is (position q // CG, group q % CG); positions outside
+    the row or rows outside the volume load zeros."""
+    cg_n = cs // 8
+    pps = 2 * nc + 1
+    for q in range(seg * cg_n):
+        pos, cg = divmod(q, cg_n)
+        slot = pos * pps + cg
+        assert 0 <= slot < wslots and pos < segmax
+        w = s0 + pos
+        if row is not None and 0 <= w < sw_len:
+            lds[slot] = src[n, row[0], row[1], w, 8 * cg:8 * cg + 8]
+        else:
+            lds[slot] = 0.0
+
+
+def replay_fwd(x, wt, stride, pad, mb, sw):
+    """strided_fwd_rs_kernel on NDHWC float64 x [n, D, H, W, Cs]; weight OIDHW."""
+    n_, D, H, W, cs = x.shape
+    co = wt.shape[0]
+    nc = (cs + 15) // 16
+    sd, sh, _ = stride
+    pd, ph, pw = pad
+    OD, OH, OW = ((v + 2 * p - 3) // s + 1 for v, p, s in zip((D, H, W), pad, stride))
+    segp = (32 * mb - 1) * sw + 3
+    pps = 2 * nc + 1
+    p_epi = 32 * ((co + 31) // 32) + 8
+    wslots = max(segp * pps, 4 * p_epi)
+    nwb = -(-OW // (32 * mb))
+    # packed weights: fragment (c16, tap) lane (li = co, g) -> W[co][16 c16 + 8 g + e][tap]
+    wk = np.zeros((nc * 16, 27, co))
+    wk[:cs] = wt.reshape(co, cs, 27).transpose(1, 2, 0)
+    y = np.zeros((n_, OD, OH, OW, co))
+    for n, od, oh, wb in itertools.product(range(n_), range(OD), range(OH), range(nwb)):
+        ow0 = wb * mb * 32
+        iw0 = ow0 * sw - pw
+        lds = np.zeros((wslots, 8))
+        for pos in range(segp):  # K-padding groups stay zero
+            for cg in range(cs // 8, 2 * nc):
+                lds[pos * pps + cg] = 0.0
+        acc = np.zeros((mb, 32, co))
+        for st in range(9):
+            kd, kh = divmod(st, 3)
+            idd, ih = od * sd - pd + kd, oh * sh - ph + kh
+            row = (idd, ih) if (0 <= idd < D and 0 <= ih < H) else None
+            run_segment_tile(lds, wslots, x, n, row, iw0, segp, segp, nc, cs, W)
+            for kw, c in itertools.product(range(3), range(nc)):
+                t = st * 3 + kw
+                for m in range(mb):
+                    li = np.arange(32)
+                    frag = np.concatenate([lds[((m * 32 + li) * sw + kw) * pps + 2 * c + g] for g in (0, 1)], axis=1)
+                    slots = ((m * 32 + li) * sw + kw) * pps + 2 * c + 1
+                    assert slots.max() < wslots
+                    acc[m] += frag @ wk[16 * c:16 * c + 16, t, :]
+        for m in range(mb):
+            for li in range(32):
+                ow = ow0 + 32 * m + li
+                if ow < OW:
+                    y[n, od, oh, ow] = acc[m, li]
+    return y
+
+
+def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
+    """strided_dx_rs_kernel on NDHWC float64 dY [n, OD, OH, OW, Cs = Cout]; weight OIDHW."""
+    n_, OD, OH, OW, cs = dy.shape
+    _, ci, D, H, W = x_shape
+    nc = (cs + 15) // 16
+    sd, sh, _ = stride
+    pd, ph, pw = pad
+    segmax = 32 * mb + 2
+    pps = 2 * nc + 1
+    p_epi = 32 * ((ci + 31) // 32) + 8
+    wslots = max(segmax * pps, 4 * p_epi)
+    nwb = -(-(-(-W // sw)) // (32 * mb))
+    # dX packing (strided_pack_kernel): K channel = Cout index, column = Cin index, tap t as is
+    wk = np.zeros((nc * 16, 27, ci))
+    wk[:cs] = wt.reshape(cs, ci, 27).transpose(0, 2, 1)
+    dx = np.zeros((n_, D, H, W, ci))
+    for n, rd, rh, res, wb in itertools.product(range(n_), range(D), range(H), range(sw), range(nwb)):
+        td = tap_range(True, rd, pd, sd)
+        th = tap_range(True, rh, ph, sh)
+        tw = tap_range(True, res, pw, sw)
+        j0 = wb * mb * 32
+        seg = 32 * mb + (tw[2] - 1 if tw[2] > 0 else 0)
+        s0 = j0 + tw[3] - (tw[2] - 1 if tw[2] > 0 else 0)
+        assert seg <= segmax
+        lds = np.zeros((wslots, 8))
+        acc = np.zeros((mb, 32, ci))
+        for md, mh in itertools.product(range(td[2]), range(th[2])):
+            cd, ch = td[3] + md * td[4], th[3] + mh * th[4]
+            kd, kh = td[0] + md * td[1], th[0] + mh * th[1]
+            row = (cd, ch) if (0 <= cd < OD and 0 <= ch < OH) else None
+            run_segment_tile(lds, wslots, dy, n, row, s0, seg, segmax, nc, cs, OW)
+            for mw in range(tw[2]):
+                kw = tw[0] + mw * tw[1]
+                t = (kd * 3 + kh) * 3 + kw
+                pb = tw[2] - 1 - mw
+                for c, m in itertools.product(range(nc), range(mb)):
+                    li = np.arange(32)
+                    pos = m * 32 + li + pb
+                    assert pos.max() < seg
+                    frag = np.concatenate([lds[pos * pps + 2 * c + g] for g in (0, 1)], axis=1)
+                    acc[m] += frag @ wk[16 * c:16 * c + 16, t, :]
+        for m in range(mb):
+            for li in range(32):
+                w = res + sw * (j0 + 32 * m + li)
+                if w < W:
+                    dx[n, rd, rh, w] = acc[m, li]
+    return dx
+
+
+@pytest.mark.parametrize("mb", [1, 2])
+@pytest.mark.parametrize("sw", [1, 2])
+@pytest.mark.parametrize("cs", [8, 24, 32])
+def test_fwd_row_segments_match_conv3d(mb, sw, cs):
+    rng = np.random.default_rng(7 * mb + sw + cs)
+    stride, pad = (2, 1, sw), (1, 0, 1)
+    x = rng.standard_normal((1, cs, 4, 4, 70))
+    wt = rng.standard_normal((5, cs, 3, 3, 3))
+    ref = F.conv3d(torch.from_numpy(x), torch.from_numpy(wt), None, stride, pad).numpy()
+    y = replay_fwd(x.transpose(0, 2, 3, 4, 1).copy(), wt, stride, pad, mb, sw)
+    np.testing.assert_allclose(y.transpose(0, 4, 1, 2, 3), ref, rtol=1e-12, atol=1e-10)
+
+
+@pytest.mark.parametrize("mb", [1, 2])
+@pytest.mark.parametrize("sw", [1, 2])
+@pytest.mark.parametrize("cs", [8, 40, 64])
+def test_dx_row_segments_match_conv3d_input_grad(mb, sw, cs):
+    rng = np.random.default_rng(11 * mb + sw + cs)
+    stride, pad = (2, 1, sw), (1, 1, 1)
+    ci = 6
+    x_shape = (1, ci, 5, 3, 67)
+    wt = rng.standard_normal((cs, ci, 3, 3, 3))
+    y_shape = (1, cs) + tuple((v + 2 * p - 3) // s + 1 for v, p, s in zip(x_shape[2:], pad, stride))
+    dy = rng.standard_normal(y_shape)
+    ref = torch.nn.grad.conv3d_input(x_shape, torch.from_numpy(wt), torch.from_numpy(dy), stride, pad).numpy()
+    dx = replay_dx(dy.transpose(0, 2, 3, 4, 1).copy(), wt, x_shape, stride, pad, mb, sw)
+    np.testing.assert_allclose(dx.transpose(0, 4, 1, 2, 3), ref, rtol=1e-12, atol=1e-10)
