@@ -121,7 +121,8 @@ int32_t r3c_conv3d_dw(const r3c_conv_desc* desc, const void* x, const void* dy,
  * is a Conv3d descriptor whose output dims are (in + 2 pad - k) / stride + 1,
  * kernel 1 or 3, any x / y strides.  Forward and dX: a direct kernel (tiles
  * of one residue class of w for dX; for k = 3, w stride 1 or 2 and up to 32
- * (forward) or 64 (dX) source channels, the source rows staged through LDS);
+ * (forward, NCDHW read in place when W % 8 == 0) or 64 (dX) source channels,
+ * the source rows staged through LDS);
  * dW + db: a direct kernel for k = 3, w
  * stride 1 or 2, w padding 1, w-contiguous 16-byte aligned rows with W % 8 ==
  * 0 and OW % 16 == 0 (dense NDHWC operands with channels and positions

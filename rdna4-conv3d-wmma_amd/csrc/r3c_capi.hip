@@ -1736,6 +1736,21 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   plan_strided(d, st, dx, p);
   if (p.a.ntiles / 4 >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "strided Conv3d: too many output tiles");
   if (p.copy_bytes && (reinterpret_cast<uintptr_t>(src) & 15)) p.copy_bytes = 0;  // unaligned: 2-byte loads
+  // Forward, k = 3, w stride 1 or 2, an NCDHW source (w-contiguous rows of a
+  // multiple of 8, at most 32 channels) and at most two column blocks: the
+  // row-segment kernel reads the source in place (no NDHWC copy).
+  {
+    const int64_t* ss = p.a.ss;
+    const bool cf = !dx && p.a.k == 3 && !p.a.scl && (p.a.sw == 1 || p.a.sw == 2) && p.nb <= 2 &&
+                    p.a.Cs % 8 == 0 && p.a.Cs <= 32 && ss[4] == 1 && p.a.Sw % 8 == 0 && ss[3] % 8 == 0 &&
+                    ss[2] % 8 == 0 && ss[1] % 8 == 0 && ss[0] % 8 == 0 &&
+                    (int64_t)(p.a.Cs - 1) * ss[1] + p.a.Sw < (1ll << 31) &&
+                    (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    if (cf) {
+      p.a.chan_first = p.a.Cs / 8;
+      p.copy_bytes = 0;
+    }
+  }
   const int64_t need = p.wpk_bytes + p.copy_bytes;
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
@@ -1774,7 +1789,7 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
     const int64_t per_w = (dx ? cdiv(a.Rw, a.sw) : a.Rw);
     const int nwb2 = (int)cdiv(per_w, 64);
     const int64_t nt2 = a.ntiles / a.nwb * nwb2;
-    if (a.scl && p.nb <= 2 && (nt2 + 3) / 4 >= 8ll * kNumCUs) {
+    if ((a.scl || a.chan_first) && p.nb <= 2 && (nt2 + 3) / 4 >= 8ll * kNumCUs) {
       a.mb = 2;
       a.nwb = nwb2;
       a.ntiles = nt2;
@@ -1787,7 +1802,7 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   // dX likewise with dY row segments (at most 64 dY channels).
   const bool seg_ok = a.k == 3 && a.scl && (a.sw == 1 || a.sw == 2) && p.nb <= 2 &&
                       (int64_t)a.Sw * a.ss[4] < (1ll << 31);
-  const bool rs = seg_ok && !dx && a.nc16 <= 2;
+  const bool rs = (seg_ok || a.chan_first) && !dx && a.nc16 <= 2;
   const bool dxrs = seg_ok && dx && a.nc16 <= 4;
   TimedLaunch tl(KIND_ROW, s);
   const bool launched = rs     ? launch_strided_fwd_rs(d->dtype, p.nb, a, s)

@@ -319,6 +319,7 @@ struct StridedArgs {
   int32_t scl;           // 1: source channel-contiguous, 16-byte aligned, Cs % 8 == 0
   int32_t dvec4;         // 1: destination channel-contiguous, Cd % 4 == 0, 8-byte aligned
   int32_t mb;            // blocks of 32 destination positions per wave (1, or 2 with scl)
+  int32_t chan_first;    // row-segment forward on an NCDHW source: its 8-channel groups (1 .. 4), else 0
   int32_t dtile;         // 1: forward, one column tile, destination channel-contiguous with positions Cd
                          // apart, Cd % 8 == 0, 16-byte aligned: a tile is one contiguous run, stored
                          // through LDS as 16-byte chunks

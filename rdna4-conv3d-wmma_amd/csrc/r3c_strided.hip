@@ -305,14 +305,22 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 // epilogue as in strided_kernel.
 // At least 3 waves per SIMD (the register cap it implies, 168, holds every
 // instantiation without spills; measured 146 -> 132 us at the bench shape).
-template <typename T, int NB, int MB, int SW, int NC>
+// CF = 0: channel-contiguous source.  CF = 1 .. 4: an NCDHW source with CF
+// 8-channel groups (Cs = 8 CF, W % 8 == 0), read in place: a lane item is
+// (8 aligned positions, 8-channel group), eight 16-byte loads of one row run
+// per channel, transposed in registers (v_perm) into 8 position slots, as
+// the tap kernel stages NCDHW tiles.
+template <typename T, int NB, int MB, int SW, int NC, int CF>
 __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArgs a) {
   constexpr int SEGP = (32 * MB - 1) * SW + 3;  // positions of a row segment
   constexpr int PPS = 2 * NC + 1;                // slots (16 bytes) per position
   constexpr int SEGSLOTS = SEGP * PPS;
   constexpr int P = 32 * NB + 8;                 // epilogue pitch (halves)
   constexpr int WSLOTS = SEGSLOTS > 4 * P ? SEGSLOTS : 4 * P;
-  constexpr int NQ = (SEGP * 2 * NC + 63) / 64;  // 16-byte chunks per lane per segment (upper bound)
+  constexpr int NQ = CF ? 1 : (SEGP * 2 * NC + 63) / 64;   // channel-last chunks per lane (upper bound)
+  constexpr int NS8 = (SEGP + 14) / 8;                      // CF: 8-position runs covering a segment
+  constexpr int NQC = CF ? (NS8 * CF + 63) / 64 : 1;        // CF: items per lane
+  static_assert(!CF || (CF + 1) / 2 == NC, "CF channel groups fill NC 16-channel blocks");
   __shared__ uint4 s_seg[4 * WSLOTS];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -336,38 +344,93 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
   uint4* sb = s_seg + wv * WSLOTS;
 
   // Channel-group slots past Cs (K padding of the last block) stay zero.
-  const int CG = a.Cs >> 3;  // 8-channel groups present (Cs % 8 == 0)
+  const int CG = CF ? CF : a.Cs >> 3;  // 8-channel groups present (Cs % 8 == 0)
   for (int q = lane; q < SEGP * (2 * NC - CG); q += 64) {
     const int pos = q / (2 * NC - CG), cg = CG + q % (2 * NC - CG);
     sb[pos * PPS + cg] = make_uint4(0u, 0u, 0u, 0u);
   }
-  // This lane's chunks of a segment: element offset within the row (-1: none
-  // or outside the row) and LDS slot.
+  // Channel-last: this lane's chunks of a segment, element offset within the
+  // row (-1: none or outside the row) and LDS slot.
   int goff[NQ], loff[NQ];
+  // CF: this lane's items, element offset of channel 8 cg at the run's first
+  // position (-1: none or outside the row), first segment position (may be
+  // below 0) and channel group.
+  int coff[NQC], cpos[NQC], ccg[NQC];
+  const int a0 = iw0 - (((iw0 % 8) + 8) % 8);  // iw0 rounded down to a multiple of 8
+  if constexpr (!CF) {
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    const int q = lane + 64 * i;
-    const int pos = q / CG, cg = q - (q / CG) * CG;
-    const int iw = iw0 + pos;
-    const bool in = q < SEGP * CG;
-    loff[i] = in ? pos * PPS + cg : -1;
-    goff[i] = (in && (unsigned)iw < (unsigned)a.Sw) ? (int)((int64_t)iw * a.ss[4]) + 8 * cg : -1;
+    for (int i = 0; i < NQ; ++i) {
+      const int q = lane + 64 * i;
+      const int pos = q / CG, cg = q - (q / CG) * CG;
+      const int iw = iw0 + pos;
+      const bool in = q < SEGP * CG;
+      loff[i] = in ? pos * PPS + cg : -1;
+      goff[i] = (in && (unsigned)iw < (unsigned)a.Sw) ? (int)((int64_t)iw * a.ss[4]) + 8 * cg : -1;
+    }
+  } else {
+    const int ns8 = (iw0 - a0 + SEGP + 7) >> 3;
+#pragma unroll
+    for (int i = 0; i < NQC; ++i) {
+      const int it = lane + 64 * i;
+      const int ps = it / CF, cg = it - (it / CF) * CF;
+      const int w8 = a0 + 8 * ps;
+      const bool in = it < ns8 * CF;
+      cpos[i] = in ? w8 - iw0 : SEGP;  // SEGP: no position of it is stored
+      ccg[i] = cg;
+      coff[i] = (in && w8 >= 0 && w8 < a.Sw) ? w8 + (int)(8 * cg * a.ss[1]) : -1;
+    }
   }
   const uint16_t* src = a.src + (int64_t)n * a.ss[0];
   uint4 pf[NQ];
+  uint4 pc[NQC][8];
   auto issue = [&](int st) __attribute__((always_inline)) {
     const int kd = st / 3, kh = st - (st / 3) * 3;
     const int id = rd * a.sd - a.pd + kd, ih = rh * a.sh - a.ph + kh;
     const bool row_ok = (unsigned)id < (unsigned)a.Sd && (unsigned)ih < (unsigned)a.Sh;
     const uint16_t* rowp = src + (int64_t)id * a.ss[2] + (int64_t)ih * a.ss[3];
+    if constexpr (!CF) {
 #pragma unroll
-    for (int i = 0; i < NQ; ++i)
-      pf[i] = (row_ok && goff[i] >= 0) ? *reinterpret_cast<const uint4*>(rowp + goff[i]) : make_uint4(0u, 0u, 0u, 0u);
+      for (int i = 0; i < NQ; ++i)
+        pf[i] = (row_ok && goff[i] >= 0) ? *reinterpret_cast<const uint4*>(rowp + goff[i]) : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NQC; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pc[i][e] = (row_ok && coff[i] >= 0)
+                         ? *reinterpret_cast<const uint4*>(rowp + coff[i] + (int64_t)e * a.ss[1])
+                         : make_uint4(0u, 0u, 0u, 0u);
+    }
   };
   auto commit = [&]() __attribute__((always_inline)) {
+    if constexpr (!CF) {
 #pragma unroll
-    for (int i = 0; i < NQ; ++i)
-      if (loff[i] >= 0) sb[loff[i]] = pf[i];
+      for (int i = 0; i < NQ; ++i)
+        if (loff[i] >= 0) sb[loff[i]] = pf[i];
+    } else {
+      // 8 channels x 8 positions -> 8 slots of 8 channels (position p of
+      // channel e is half p of pc[e]).
+#pragma unroll
+      for (int i = 0; i < NQC; ++i)
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const int pos = cpos[i] + p;
+          if ((unsigned)pos >= (unsigned)SEGP) continue;
+          const uint32_t sel = (p & 1) ? 0x07060302u : 0x05040100u;
+          const int m = p >> 1;
+          uint4 v;
+          uint32_t* vv = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint4& lo = pc[i][2 * q];
+            const uint4& hi = pc[i][2 * q + 1];
+            const uint32_t l = m == 0 ? lo.x : (m == 1 ? lo.y : (m == 2 ? lo.z : lo.w));
+            const uint32_t h = m == 0 ? hi.x : (m == 1 ? hi.y : (m == 2 ? hi.z : hi.w));
+            vv[q] = __builtin_amdgcn_perm(h, l, sel);
+          }
+          sb[pos * PPS + ccg[i]] = v;
+        }
+    }
   };
 
   f32x16_t acc[MB][NB];
@@ -869,12 +932,17 @@ bool launch_t(const StridedArgs& a, int nb, hipStream_t s) {
 
 template <typename T, int NB, int MB>
 bool launch_rs_sw(const StridedArgs& a, int nc, unsigned blocks, hipStream_t s) {
-  if (a.sw == 1 && nc == 1) hipLaunchKernelGGL((strided_fwd_rs_kernel<T, NB, MB, 1, 1>), dim3(blocks), dim3(256), 0, s, a);
-  else if (a.sw == 1 && nc == 2) hipLaunchKernelGGL((strided_fwd_rs_kernel<T, NB, MB, 1, 2>), dim3(blocks), dim3(256), 0, s, a);
-  else if (a.sw == 2 && nc == 1) hipLaunchKernelGGL((strided_fwd_rs_kernel<T, NB, MB, 2, 1>), dim3(blocks), dim3(256), 0, s, a);
-  else if (a.sw == 2 && nc == 2) hipLaunchKernelGGL((strided_fwd_rs_kernel<T, NB, MB, 2, 2>), dim3(blocks), dim3(256), 0, s, a);
-  else return false;
-  return true;
+#define R3C_RS(SW_, NC_, CF_) \
+  if (a.sw == SW_ && nc == NC_ && cf == CF_) { \
+    hipLaunchKernelGGL((strided_fwd_rs_kernel<T, NB, MB, SW_, NC_, CF_>), dim3(blocks), dim3(256), 0, s, a); \
+    return true; \
+  }
+  const int cf = a.chan_first;
+  R3C_RS(1, 1, 0) R3C_RS(1, 2, 0) R3C_RS(2, 1, 0) R3C_RS(2, 2, 0)
+  R3C_RS(1, 1, 1) R3C_RS(1, 1, 2) R3C_RS(1, 2, 3) R3C_RS(1, 2, 4)
+  R3C_RS(2, 1, 1) R3C_RS(2, 1, 2) R3C_RS(2, 2, 3) R3C_RS(2, 2, 4)
+#undef R3C_RS
+  return false;
 }
 template <typename T>
 bool launch_rs_t(const StridedArgs& a, int nb, hipStream_t s) {

@@ -58,6 +58,7 @@ CASES = [
     # dX through LDS dY row segments with two column blocks (Cin 33-64)
     (1, 40, 32, 6, 10, 32, 3, (1, 1, 1), (2, 2, 2)),
     (1, 48, 24, 5, 6, 16, 3, (1, 1, 1), (1, 1, 1)),      # stride 1 through the strided entry points
+    (1, 32, 40, 6, 8, 64, 3, (1, 1, 1), (2, 2, 2)),      # forward row segments on 4 channel groups
 ]
 
 

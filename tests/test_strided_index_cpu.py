@@ -1,5 +1,6 @@
 """Index math of the strided kernels that stage source rows through LDS
-(csrc/r3c_strided.hip: strided_fwd_rs_kernel, strided_dx_rs_kernel),
+(csrc/r3c_strided.hip: strided_fwd_rs_kernel with an NDHWC source or an
+NCDHW one read in place, strided_dx_rs_kernel),
 replayed on the CPU with numpy and checked against PyTorch's float64
 convolution, with every LDS slot and every source element the replay touches
 asserted inside its buffer.
@@ -48,9 +49,37 @@ def run_segment_tile(lds, wslots, src, n, row, s0, seg, segmax, nc, cs, sw_len):
             lds[slot] = 0.0
 
 
-def replay_fwd(x, wt, stride, pad, mb, sw):
-    """strided_fwd_rs_kernel on NDHWC float64 x [n, D, H, W, Cs]; weight OIDHW."""
-    n_, D, H, W, cs = x.shape
+def run_segment_tile_cf(lds, wslots, src, n, row, iw0, segp, nc, cs, sw_len):
+    """The same segment from an NCDHW source read in place (CF): lane item
+    (8 aligned positions from a0 = iw0 rounded down to a multiple of 8,
+    8-channel group) loads 8 channels x 8 positions and stores position
+    a0 + 8 ps + p at segment position a0 + 8 ps + p - iw0 when inside."""
+    cg_n = cs // 8
+    pps = 2 * nc + 1
+    a0 = iw0 - (iw0 % 8)
+    ns8 = (iw0 - a0 + segp + 7) // 8
+    for it in range(ns8 * cg_n):
+        ps, cg = divmod(it, cg_n)
+        w8 = a0 + 8 * ps
+        loaded = row is not None and 0 <= w8 < sw_len
+        if loaded:
+            assert w8 + 7 < sw_len
+            block = src[n, 8 * cg:8 * cg + 8, row[0], row[1], w8:w8 + 8]  # [channel][position]
+        for p in range(8):
+            pos = w8 + p - iw0
+            if 0 <= pos < segp:
+                slot = pos * pps + cg
+                assert slot < wslots
+                lds[slot] = block[:, p] if loaded else 0.0
+
+
+def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
+    """strided_fwd_rs_kernel on float64 x, NDHWC [n, D, H, W, Cs] (CF 0) or
+    NCDHW [n, Cs, D, H, W] read in place (CF = Cs / 8); weight OIDHW."""
+    if channels_first:
+        n_, cs, D, H, W = x.shape
+    else:
+        n_, D, H, W, cs = x.shape
     co = wt.shape[0]
     nc = (cs + 15) // 16
     sd, sh, _ = stride
@@ -77,7 +106,10 @@ def replay_fwd(x, wt, stride, pad, mb, sw):
             kd, kh = divmod(st, 3)
             idd, ih = od * sd - pd + kd, oh * sh - ph + kh
             row = (idd, ih) if (0 <= idd < D and 0 <= ih < H) else None
-            run_segment_tile(lds, wslots, x, n, row, iw0, segp, segp, nc, cs, W)
+            if channels_first:
+                run_segment_tile_cf(lds, wslots, x, n, row, iw0, segp, nc, cs, W)
+            else:
+                run_segment_tile(lds, wslots, x, n, row, iw0, segp, segp, nc, cs, W)
             for kw, c in itertools.product(range(3), range(nc)):
                 t = st * 3 + kw
                 for m in range(mb):
@@ -143,16 +175,20 @@ def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
     return dx
 
 
+@pytest.mark.parametrize("layout", ["ndhwc", "ncdhw"])
 @pytest.mark.parametrize("mb", [1, 2])
 @pytest.mark.parametrize("sw", [1, 2])
 @pytest.mark.parametrize("cs", [8, 24, 32])
-def test_fwd_row_segments_match_conv3d(mb, sw, cs):
+def test_fwd_row_segments_match_conv3d(mb, sw, cs, layout):
     rng = np.random.default_rng(7 * mb + sw + cs)
     stride, pad = (2, 1, sw), (1, 0, 1)
-    x = rng.standard_normal((1, cs, 4, 4, 70))
+    x = rng.standard_normal((1, cs, 4, 4, 72))  # W % 8 == 0 (in-place NCDHW reads whole 8-position runs)
     wt = rng.standard_normal((5, cs, 3, 3, 3))
     ref = F.conv3d(torch.from_numpy(x), torch.from_numpy(wt), None, stride, pad).numpy()
-    y = replay_fwd(x.transpose(0, 2, 3, 4, 1).copy(), wt, stride, pad, mb, sw)
+    if layout == "ncdhw":
+        y = replay_fwd(x, wt, stride, pad, mb, sw, channels_first=True)
+    else:
+        y = replay_fwd(x.transpose(0, 2, 3, 4, 1).copy(), wt, stride, pad, mb, sw)
     np.testing.assert_allclose(y.transpose(0, 4, 1, 2, 3), ref, rtol=1e-12, atol=1e-10)
 
 
