@@ -1726,6 +1726,16 @@ void plan_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, StridedPla
   p.copy_bytes = !a.scl && ncdhw_copyable(ss, a.Cs, a.Sd, a.Sh, a.Sw)
                      ? align256(tensor_bytes(d->n, a.Cs, a.Sd, a.Sh, a.Sw))
                      : 0;
+  // Forward, k = 3, w stride 1 or 2, an NCDHW source (w-contiguous rows of a
+  // multiple of 8, at most 32 channels) and at most two column blocks: the
+  // row-segment kernel reads the source in place, no NDHWC copy (with an
+  // unaligned source the run falls back to 2-byte gathers, also without it).
+  if (!dx && a.k == 3 && !a.scl && (a.sw == 1 || a.sw == 2) && p.nb <= 2 && a.Cs % 8 == 0 && a.Cs <= 32 &&
+      ss[4] == 1 && a.Sw % 8 == 0 && ss[3] % 8 == 0 && ss[2] % 8 == 0 && ss[1] % 8 == 0 && ss[0] % 8 == 0 &&
+      (int64_t)(a.Cs - 1) * ss[1] + a.Sw < (1ll << 31)) {
+    a.chan_first = a.Cs / 8;
+    p.copy_bytes = 0;
+  }
 }
 
 int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* src, const void* w, const void* bias,
@@ -1736,21 +1746,7 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
   plan_strided(d, st, dx, p);
   if (p.a.ntiles / 4 >= (1ll << 31)) return fail(R3C_UNSUPPORTED, "strided Conv3d: too many output tiles");
   if (p.copy_bytes && (reinterpret_cast<uintptr_t>(src) & 15)) p.copy_bytes = 0;  // unaligned: 2-byte loads
-  // Forward, k = 3, w stride 1 or 2, an NCDHW source (w-contiguous rows of a
-  // multiple of 8, at most 32 channels) and at most two column blocks: the
-  // row-segment kernel reads the source in place (no NDHWC copy).
-  {
-    const int64_t* ss = p.a.ss;
-    const bool cf = !dx && p.a.k == 3 && !p.a.scl && (p.a.sw == 1 || p.a.sw == 2) && p.nb <= 2 &&
-                    p.a.Cs % 8 == 0 && p.a.Cs <= 32 && ss[4] == 1 && p.a.Sw % 8 == 0 && ss[3] % 8 == 0 &&
-                    ss[2] % 8 == 0 && ss[1] % 8 == 0 && ss[0] % 8 == 0 &&
-                    (int64_t)(p.a.Cs - 1) * ss[1] + p.a.Sw < (1ll << 31) &&
-                    (reinterpret_cast<uintptr_t>(src) & 15) == 0;
-    if (cf) {
-      p.a.chan_first = p.a.Cs / 8;
-      p.copy_bytes = 0;
-    }
-  }
+  if (p.a.chan_first && (reinterpret_cast<uintptr_t>(src) & 15)) p.a.chan_first = 0;  // unaligned: 2-byte loads
   const int64_t need = p.wpk_bytes + p.copy_bytes;
   if (ws_bytes < need)
     return fail(R3C_INVALID, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
