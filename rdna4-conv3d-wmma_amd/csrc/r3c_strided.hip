@@ -291,9 +291,8 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
   }
 }
 
-// Forward, k = 3, w stride SW (1 or 2), channel-contiguous source with at
-// most 32 channels (NC 16-channel blocks): the x operand through the wave's
-// LDS.  Per (kd, kh) the wave's input row segment (the SEGP positions its
+// Forward, k = 3, w stride SW (1 or 2), at most 32 source channels (NC
+// 16-channel blocks): the x operand through the wave's LDS.  Per (kd, kh) the wave's input row segment (the SEGP positions its
 // 32 MB outputs read for kw = 0 .. 2) is loaded with 16-byte loads of
 // consecutive (position, 8-channel group) chunks -- whole row runs when
 // positions are contiguous, instead of one 16-byte fragment at each of 32
@@ -302,9 +301,8 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 // The three kw taps then read their fragments from LDS.  The next row
 // segment is in registers while the current one is multiplied; LDS is
 // private to the wave (in-order LDS, no barrier).  Weights, tile order and
-// epilogue as in strided_kernel.
-// At least 3 waves per SIMD (the register cap it implies, 168, holds every
-// instantiation without spills; measured 146 -> 132 us at the bench shape).
+// epilogue as in strided_kernel.  At least 3 waves per SIMD: the register
+// cap that implies (168) holds every instantiation without spills.
 // CF = 0: channel-contiguous source.  CF = 1 .. 4: an NCDHW source with CF
 // 8-channel groups (Cs = 8 CF, W % 8 == 0), read in place: a lane item is
 // (8 aligned positions, 8-channel group), eight 16-byte loads of one row run
