@@ -400,7 +400,8 @@ def strided_passes(layout: str, reps: int = 10):
     bf16.  Native: median of the summed kernel durations of each pass (HIP
     events on the launch stream, MALL flushed as in hbm_passes).  Stock:
     F.conv3d / torch.nn.grad on the same tensors, CUDA events around the call.
-    TFLOP/s on the algorithmic 2 N OD OH OW Cout Cin 27."""
+    TFLOP/s on the algorithmic 2 N OD OH OW Cout Cin 27; frac_hbm on the
+    compulsory |x| + |y| bytes (the bound at this shape: 130 FLOP per byte)."""
     import torch
     import torch.nn.functional as F
     from rdna4_conv3d import _native as nat
@@ -463,11 +464,14 @@ def strided_passes(layout: str, reps: int = 10):
         "dx": lambda: torch.nn.grad.conv3d_input(x.shape, wt, go, st, pd),
         "dw": lambda: torch.nn.grad.conv3d_weight(x, wt.shape, go, st, pd),
     }
+    # compulsory HBM bytes: the pass's two activation tensors (the weight is 62 KB)
+    act_bytes = (x.numel() + go.numel()) * 2
     out = {}
     for p in ("fwd", "dx", "dw"):
         ms_n, ms_s = native_ms(native[p]), stock_ms(stock[p])
         out[f"k3s2_{ci}to{co}_{d}x{h}x{w}_bf16_{p}"] = {
             "us": round(ms_n * 1e3, 2), "tflops": round(flops / (ms_n * 1e-3) / 1e12, 1),
+            "frac_hbm": round(act_bytes / (ms_n * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "stock_us": round(ms_s * 1e3, 2), "stock_tflops": round(flops / (ms_s * 1e-3) / 1e12, 1)}
     del x, go, wt, flush, flush_rd
     torch.cuda.empty_cache()
