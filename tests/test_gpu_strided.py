@@ -7,6 +7,13 @@ is the opt-in widening (rdna4_conv3d.strided).  Tolerances are the north
 star's: max|out - ref| / max|ref| <= 1e-2 for forward and dX, <= 3e-2 for dW
 and db.  The library's timing hook must record the strided kernels, so a stock
 fallback cannot pass.
+
+The cases reach every kernel path: the gathering kernel (ragged channels,
+stride 3, k=1, more than two column blocks), the LDS row-segment forward on
+NDHWC sources and on NCDHW sources read in place (8-32 channels), the
+row-segment dX (dY up to 64 channels), the direct dW on NCDHW operands and on
+NCDHW copies of NDHWC ones, and the dY-scatter dW for the rest; the full-size
+cases add two position blocks per wave.
 """
 from __future__ import annotations
 
