@@ -7,7 +7,10 @@ trunk k=3 layers of BASELINE config 2, bf16 inputs, fp32 accumulation, inputs
 already resident in HBM:
     [4,24,64,128,128]->24, [4,48,32,64,64]->48, [4,96,16,32,32]->96, [4,192,8,16,16]->192
 value = algorithmic FLOPs of the step (3 passes x 2*N*D*H*W*Cin*Cout*27 per layer)
-        / measured step time, in TFLOP/s.
+        / measured step time, in TFLOP/s.  Order: W warmup steps, --preheat
+        seconds of further untimed steps (clocks at steady state; reported as
+        preheat_s / preheat_steps), the per-pass profile steps, then exactly K
+        timed steps.
 
 Also reported on the same JSON line:
   roofline      the dominant kernel (largest share of the step): algorithmic FLOPs
@@ -25,7 +28,8 @@ Also reported on the same JSON line:
                 compulsory HBM bytes / time vs 8 TB/s.
   strided_passes  the strided Conv3d (k=3 stride 2, [4,24,64,128,128] -> 48,
                 bf16; outside the reference's stride-1 policy): native and stock
-                (MIOpen) time per pass and TFLOP/s on the algorithmic FLOPs.
+                (MIOpen) time per pass, TFLOP/s on the algorithmic FLOPs and the
+                fraction of HBM peak on the compulsory activation bytes.
   cpu_baseline  the reference's CPU path (Conv3dWmma on CPU tensors ->
                 nn.Conv3d.forward -> F.conv3d, oneDNN, fp32) on a bounded sample.
 
@@ -37,7 +41,8 @@ Also reported on the same JSON line:
                 unet3d_base32 the same at base=32; with --unet-fp16, unet3d_fp16
                 the same at base=24 under fp16 autocast (the reference's protocol).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout ncdhw|ndhwc] [--unet-steps S]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--preheat SEC] [--layout ncdhw|ndhwc]
+                       [--unet-steps S] [--unet-fp16]
 """
 from __future__ import annotations
 
