@@ -1785,7 +1785,10 @@ int run_strided(const r3c_conv_desc* d, const int32_t* st, bool dx, const void* 
     const int64_t per_w = (dx ? cdiv(a.Rw, a.sw) : a.Rw);
     const int nwb2 = (int)cdiv(per_w, 64);
     const int64_t nt2 = a.ntiles / a.nwb * nwb2;
-    if ((a.scl || a.chan_first) && p.nb <= 2 && (nt2 + 3) / 4 >= 8ll * kNumCUs) {
+    // (an NCDHW forward source of 4 channel groups with 2 column blocks keeps
+    // one block: two would spill registers)
+    const bool cf_spill = !dx && a.chan_first == 4 && p.nb == 2;
+    if ((a.scl || a.chan_first) && p.nb <= 2 && !cf_spill && (nt2 + 3) / 4 >= 8ll * kNumCUs) {
       a.mb = 2;
       a.nwb = nwb2;
       a.ntiles = nt2;

@@ -299,15 +299,30 @@ __global__ __launch_bounds__(256) void strided_kernel(const StridedArgs a) {
 // strided positions per tap -- and stored [position][channel group] with a
 // pitch of 2 NC + 1 slots (conflict-free 16-byte reads at stride 1 or 2).
 // The three kw taps then read their fragments from LDS.  The next row
-// segment is in registers while the current one is multiplied; LDS is
-// private to the wave (in-order LDS, no barrier).  Weights, tile order and
-// epilogue as in strided_kernel.  At least 3 waves per SIMD: the register
-// cap that implies (168) holds every instantiation without spills.
+// segment is in registers while the current one is multiplied; the segment
+// block is private to the wave (in-order LDS).  The weight fragments of a
+// stage (3 kw x NC x NB) are loaded once per workgroup into shared LDS
+// between two barriers (all four waves step through the same nine stages;
+// a wave past the last tile takes part without loading or storing), the
+// next stage's in registers meanwhile.  Tile order and epilogue as in
+// strided_kernel.  At least 3 waves per SIMD: the register cap that implies
+// (168) holds every instantiation but NB 2, MB 2, CF 4 without spills (the
+// host gives that case one position block).
 // CF = 0: channel-contiguous source.  CF = 1 .. 4: an NCDHW source with CF
 // 8-channel groups (Cs = 8 CF, W % 8 == 0), read in place: a lane item is
 // (8 aligned positions, 8-channel group), eight 16-byte loads of one row run
 // per channel, transposed in registers (v_perm) into 8 position slots, as
 // the tap kernel stages NCDHW tiles.
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS
+// accesses (lgkmcnt 0) and not for its global loads, so register prefetches
+// stay in flight across it.
+__device__ __forceinline__ void lds_barrier_w() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
 template <typename T, int NB, int MB, int SW, int NC, int CF>
 __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArgs a) {
   constexpr int SEGP = (32 * MB - 1) * SW + 3;  // positions of a row segment
@@ -319,7 +334,10 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
   constexpr int NS8 = (SEGP + 14) / 8;                      // CF: 8-position runs covering a segment
   constexpr int NQC = CF ? (NS8 * CF + 63) / 64 : 1;        // CF: items per lane
   static_assert(!CF || (CF + 1) / 2 == NC, "CF channel groups fill NC 16-channel blocks");
+  constexpr int WFR = 3 * NC * NB * 64;  // weight fragments of one (kd, kh) stage
+  constexpr int WIT = (WFR + 255) / 256;  // per thread
   __shared__ uint4 s_seg[4 * WSLOTS];
+  __shared__ uint4 s_w[WFR];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5, li = lane & 31;
@@ -327,8 +345,10 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
   const int64_t nblk = gridDim.x;
   if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
   const int64_t wt = bid * 4 + wv;
-  if (wt >= a.ntiles) return;  // no barrier in this kernel
-  int64_t r = wt;
+  // Every wave stays for the workgroup barriers of the weight stages; a wave
+  // past the last tile loads nothing and stores nothing.
+  const bool tile_ok = wt < a.ntiles;
+  int64_t r = tile_ok ? wt : 0;
   const int ct = (int)(r % a.n_ctiles);
   r /= a.n_ctiles;
   const int wb = (int)(r % a.nwb);
@@ -384,7 +404,7 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
   auto issue = [&](int st) __attribute__((always_inline)) {
     const int kd = st / 3, kh = st - (st / 3) * 3;
     const int id = rd * a.sd - a.pd + kd, ih = rh * a.sh - a.ph + kh;
-    const bool row_ok = (unsigned)id < (unsigned)a.Sd && (unsigned)ih < (unsigned)a.Sh;
+    const bool row_ok = tile_ok && (unsigned)id < (unsigned)a.Sd && (unsigned)ih < (unsigned)a.Sh;
     const uint16_t* rowp = src + (int64_t)id * a.ss[2] + (int64_t)ih * a.ss[3];
     if constexpr (!CF) {
 #pragma unroll
@@ -438,12 +458,34 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[m][nb][e] = 0.f;
-  const uint4* wpk = reinterpret_cast<const uint4*>(a.wpk) + (int64_t)ct * NB * 64 + lane;
-
+  // Weight fragments of a stage: loaded by the whole workgroup into s_w
+  // ([kw][c][nb][lane]), the next stage's in registers meanwhile (one column
+  // tile: ct == 0).
+  const uint4* wsrc = reinterpret_cast<const uint4*>(a.wpk);
+  const int tid = threadIdx.x;
+  uint4 wreg[WIT];
+  auto wissue = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k2 = 0; k2 < WIT; ++k2) {
+      const int f = tid + 256 * k2;
+      const int ln = f & 63, rest = f >> 6;
+      const int nb = rest % NB, c = (rest / NB) % NC, kw = rest / (NB * NC);
+      wreg[k2] = (f < WFR && st < 9) ? wsrc[((int64_t)(c * a.taps + st * 3 + kw) * a.nbt + nb) * 64 + ln]
+                                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  (void)ct;
+  wissue(0);
   issue(0);
   commit();
   issue(1);
   for (int st = 0; st < 9; ++st) {
+    lds_barrier_w();  // every wave is done with the previous stage's weights
+#pragma unroll
+    for (int k2 = 0; k2 < WIT; ++k2)
+      if (tid + 256 * k2 < WFR) s_w[tid + 256 * k2] = wreg[k2];
+    lds_barrier_w();  // this stage's weights are in s_w
+    wissue(st + 1);
     __asm__ volatile("" ::: "memory");  // the segment's LDS writes stay ahead of its reads
     uint4 wf[3][NC][NB];
 #pragma unroll
@@ -451,7 +493,7 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) wf[kw][c][nb] = wpk[((int64_t)(c * a.taps + st * 3 + kw) * a.nbt + nb) * 64];
+        for (int nb = 0; nb < NB; ++nb) wf[kw][c][nb] = s_w[((kw * NC + c) * NB + nb) * 64 + lane];
 #pragma unroll
     for (int kw = 0; kw < 3; ++kw)
 #pragma unroll
@@ -473,6 +515,7 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
 
   // Epilogue: acc[m][nb][4q + r] = destination channel (ct NB + nb) 32 + 8 q + 4 g + r
   // at position ow0 + 32 m + li.
+  if (!tile_ok) return;
   if (a.dtile) {
     uint16_t* tb = reinterpret_cast<uint16_t*>(sb);
     const int cpp = a.Cd >> 3;
