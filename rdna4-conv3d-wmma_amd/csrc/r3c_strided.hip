@@ -363,10 +363,12 @@ __global__ __launch_bounds__(256, 3) void strided_fwd_rs_kernel(const StridedArg
 
   // Channel-group slots past Cs (K padding of the last block) stay zero.
   const int CG = CF ? CF : a.Cs >> 3;  // 8-channel groups present (Cs % 8 == 0)
-  for (int q = lane; q < SEGP * (2 * NC - CG); q += 64) {
-    const int pos = q / (2 * NC - CG), cg = CG + q % (2 * NC - CG);
-    sb[pos * PPS + cg] = make_uint4(0u, 0u, 0u, 0u);
-  }
+  const int npad = 2 * NC - CG;         // K-padding groups per position
+  if (npad > 0)
+    for (int q = lane; q < SEGP * npad; q += 64) {
+      const int pos = q / npad, cg = CG + q % npad;
+      sb[pos * PPS + cg] = make_uint4(0u, 0u, 0u, 0u);
+    }
   // Channel-last: this lane's chunks of a segment, element offset within the
   // row (-1: none or outside the row) and LDS slot.
   int goff[NQ], loff[NQ];
