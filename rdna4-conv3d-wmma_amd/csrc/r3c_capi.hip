@@ -365,8 +365,6 @@ struct RowPlan {
   int64_t ntiles;      // output tiles (box, column tile)
 };
 
-int pick_ck(int cs) { return cs <= 8 ? 8 : cs <= 16 ? 16 : cs <= 24 ? 24 : 32; }
-
 int pick_blocks(int nbt, const int* opts, int nopt) {
   int best = opts[0], best_waste = 1 << 30;
   for (int i = 0; i < nopt; ++i) {

@@ -36,7 +36,6 @@ struct PoolElem<DT_BF16> {
     }
   }
   __device__ __forceinline__ static uint16_t cvt(float v) { return from_f32<bf16_tag>(v); }
-  static constexpr int BYTES = 2;
 };
 template <>
 struct PoolElem<DT_F16> {
@@ -50,7 +49,6 @@ struct PoolElem<DT_F16> {
     }
   }
   __device__ __forceinline__ static uint16_t cvt(float v) { return from_f32<f16_tag>(v); }
-  static constexpr int BYTES = 2;
 };
 template <>
 struct PoolElem<DT_F32> {
@@ -60,7 +58,6 @@ struct PoolElem<DT_F32> {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   }
-  static constexpr int BYTES = 4;
 };
 
 // Output coordinates of thread t: (n, c, od, oh, ow0) with ow0 a multiple of 4.
