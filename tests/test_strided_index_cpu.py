@@ -1,9 +1,9 @@
 """Index math of the strided kernels that stage source rows through LDS
 (csrc/r3c_strided.hip: strided_fwd_rs_kernel with an NDHWC source or an
-NCDHW one read in place, strided_dx_rs_kernel),
-replayed on the CPU with numpy and checked against PyTorch's float64
-convolution, with every LDS slot and every source element the replay touches
-asserted inside its buffer.
+NCDHW one read in place, strided_dx_rs_kernel) and of the direct weight
+gradient (strided_dw_kernel), replayed on the CPU with numpy and checked
+against PyTorch's float64 convolution and its gradients, with every LDS slot
+and every source element the replay touches asserted inside its buffer.
 
 Per wave tile the replay follows the kernel step by step: the per-lane chunk
 table (position, 8-channel group) of a row segment, the zero-filled K-padding
@@ -11,7 +11,12 @@ slots, the LDS slot of each chunk (pitch 2 NC + 1 slots per position), the
 segment position each (block, lane, tap) fragment read uses, and the taps of
 one residue class of w for dX (tap_range).  A plausible slip -- a wrong
 segment origin, tap order, residue class or pitch -- changes the result or
-trips a bounds assertion.
+trips a bounds assertion.  For dW the replay also follows the x window's
+dword picks (v_alignbit / v_perm at 16-bit granularity), the K-block walk of
+each split with its carries and zero pipeline padding, the XCD renumbering of
+workgroups (a permutation of every (split, tile) pair), the accumulator lane
+layout of v_mfma_f32_32x32x16 and the partial write-back, every partial slot
+written exactly once.
 """
 from __future__ import annotations
 
@@ -206,3 +211,198 @@ def test_dx_row_segments_match_conv3d_input_grad(mb, sw, cs):
     ref = torch.nn.grad.conv3d_input(x_shape, torch.from_numpy(wt), torch.from_numpy(dy), stride, pad).numpy()
     dx = replay_dx(dy.transpose(0, 2, 3, 4, 1).copy(), wt, x_shape, stride, pad, mb, sw)
     np.testing.assert_allclose(dx.transpose(0, 4, 1, 2, 3), ref, rtol=1e-12, atol=1e-10)
+
+
+def _alignbit(hi, lo, shift):
+    """v_alignbit_b32 on dwords of two 16-bit elements: ({hi, lo} >> shift)[31:0]."""
+    assert shift in (0, 16)
+    return (lo[0], lo[1]) if shift == 0 else (lo[1], hi[0])
+
+
+def _perm(hi, lo, sel):
+    """v_perm_b32 byte selection on dwords of two 16-bit elements: selector
+    bytes 0-3 pick lo's bytes, 4-7 hi's; each result element must take an
+    aligned byte pair."""
+    halves = (lo[0], lo[1], hi[0], hi[1])
+    out = []
+    for r in range(2):
+        b0, b1 = (sel >> (16 * r)) & 0xFF, (sel >> (16 * r + 8)) & 0xFF
+        assert b0 % 2 == 0 and b1 == b0 + 1 and b0 < 8
+        out.append(halves[b0 // 2])
+    return tuple(out)
+
+
+def _mfma32_lanes(c):
+    """Accumulator registers of v_mfma_f32_32x32x16 for a 32 x 32 result C:
+    lane (li, g) register v holds C[8 (v // 4) + 4 g + v % 4][li]."""
+    out = np.zeros((2, 32, 16) + c.shape[2:])
+    for g, v in itertools.product(range(2), range(16)):
+        out[g, :, v] = c[8 * (v // 4) + 4 * g + v % 4]
+    return out
+
+
+def replay_dw(x, dy, stride, pad, nsplit):
+    """strided_dw_kernel plus the fixed-order reduce, on float64 NCDHW x and
+    dY (contiguous; pad w must be 1, W % 8 == 0, OW % 16 == 0).  Per wave
+    (kd, kh) and lane (li, g): the dY fragment (one 16-byte load per lane),
+    the x window (edge dword, SW aligned 16-byte loads, edge dword; zero
+    outside the row or volume), the alignbit (SW 1) / perm (SW 2) picks per kw,
+    the K-block walk with its carries and zero pipeline padding, the
+    accumulator -> (co, ci) write-back and the db of wave 0.  Returns
+    (dW OIDHW, db)."""
+    N, Cin, D, H, W = x.shape
+    _, Cout, OD, OH, OW = dy.shape
+    sd, sh, sw = stride
+    pd, ph, pw = pad
+    assert pw == 1 and W % 8 == 0 and OW % 16 == 0
+    nw = 6 if sw == 1 else 10
+    ncb = 2 if Cout > 32 else 1
+    ncg, ngb = -(-Cout // (32 * ncb)), -(-Cin // 32)
+    kpr = OW // 16
+    nkb = N * OD * OH * kpr
+    pf = 3 if ncb == 1 else 2
+    ntile = ncg * ngb
+    total = nsplit * ntile
+    part = np.full((nsplit, Cout, 27, Cin), np.nan)
+    dbpart = np.full((nsplit, Cout), np.nan)
+    hits = np.zeros(part.shape, dtype=np.int64)
+    seen = set()
+    for blk in range(total):
+        bid = (blk & 7) * (total >> 3) + (blk >> 3) if total % 8 == 0 else blk
+        seen.add(bid)
+        tile, split = bid % ntile, bid // ntile
+        cb, gb = divmod(tile, ngb)
+        k0, k1 = split * nkb // nsplit, (split + 1) * nkb // nsplit
+        li = np.arange(32)
+        ci = gb * 32 + li
+        ci_ok = ci < Cin
+        co = [(cb * ncb + c) * 32 + li for c in range(ncb)]
+        for wv in range(9):
+            kd, kh = divmod(wv, 3)
+            acc = np.zeros((ncb, 3, 32, 32))  # [nc][kw][row co][col ci]
+            dbs = np.zeros((ncb, 2, 32))       # [nc][g][li]
+            r = k0
+            kn = [r % kpr, (r // kpr) % OH, (r // kpr // OH) % OD, r // kpr // OH // OD]  # owb, oh, od, n
+
+            def advance(kp):
+                kp[0] += 1
+                if kp[0] < kpr:
+                    return
+                kp[0] = 0
+                kp[1] += 1
+                if kp[1] < OH:
+                    return
+                kp[1] = 0
+                kp[2] += 1
+                if kp[2] < OD:
+                    return
+                kp[2] = 0
+                kp[3] += 1
+
+            def load(kp, live):
+                owb, oh, od, n = kp
+                ow0 = owb * 16
+                af = np.zeros((ncb, 2, 32, 8))
+                win = np.zeros((2, 32, 2 * nw))  # [g][li][window element]
+                if not live:
+                    return af, win
+                assert n < N
+                for c in range(ncb):
+                    for g in range(2):
+                        ok = co[c] < Cout
+                        assert ow0 + 8 * g + 8 <= OW
+                        af[c, g, ok] = dy[n, co[c][ok], od, oh, ow0 + 8 * g:ow0 + 8 * g + 8]
+                idd, ih = od * sd - pd + kd, oh * sh - ph + kh
+                if not (0 <= idd < D and 0 <= ih < H):
+                    return af, win
+                for g in range(2):
+                    b = sw * (ow0 + 8 * g)
+                    rows = x[n, ci[ci_ok], idd, ih]
+                    if b >= 2:
+                        win[g, ci_ok, 0:2] = rows[:, b - 2:b]
+                    for c in range(sw):
+                        if b + 8 * c < W:
+                            assert b + 8 * c + 8 <= W
+                            win[g, ci_ok, 2 + 8 * c:10 + 8 * c] = rows[:, b + 8 * c:b + 8 * c + 8]
+                    if b + 8 * sw < W:
+                        assert b + 8 * sw + 2 <= W
+                        win[g, ci_ok, 2 * nw - 2:2 * nw] = rows[:, b + 8 * sw:b + 8 * sw + 2]
+                return af, win
+
+            def compute(frag):
+                af, win = frag
+                if wv == 0:
+                    dbs[:] += af.sum(axis=3)
+                for kw in range(3):
+                    o = kw + 1
+                    w0, odd = o >> 1, (o & 1) != 0
+                    bq = np.zeros((2, 32, 8))
+                    for g, l in itertools.product(range(2), range(32)):
+                        dw = [tuple(win[g, l, 2 * k:2 * k + 2]) for k in range(nw)]
+                        for q in range(4):
+                            if sw == 1:
+                                lo = dw[q + w0]
+                                hi = dw[q + w0 + 1] if q + w0 + 1 < nw else (0.0, 0.0)
+                                pair = _alignbit(hi, lo, 16 if odd else 0)
+                            else:
+                                lo, hi = dw[2 * q + w0], dw[2 * q + w0 + 1]
+                                pair = _perm(hi, lo, 0x07060302 if odd else 0x05040100)
+                            bq[g, l, 2 * q:2 * q + 2] = pair
+                    # MFMA 32x32x16: A[li][8 g + e] = af lane (li, g); B[8 g + e][li] = bq lane (li, g)
+                    bmat = np.concatenate([bq[0].T, bq[1].T], axis=0)  # [16][32]
+                    for c in range(ncb):
+                        amat = np.concatenate([af[c, 0], af[c, 1]], axis=1)  # [32][16]
+                        acc[c, kw] += amat @ bmat
+
+            nk = k1 - k0
+            loaded = 0
+            slots = [None] * pf
+
+            def fetch(u):
+                nonlocal loaded
+                slots[u] = load(list(kn), loaded < nk)
+                loaded += 1
+                if loaded < nk:
+                    advance(kn)
+
+            for u in range(pf):
+                fetch(u)
+            for _ in range(0, nk, pf):
+                for u in range(pf):
+                    compute(slots[u])
+                    fetch(u)
+            # write-back of each lane's registers at the kernel's (co, ci)
+            for c, kw in itertools.product(range(ncb), range(3)):
+                lanes = _mfma32_lanes(acc[c, kw])
+                t = wv * 3 + kw
+                for g, v in itertools.product(range(2), range(16)):
+                    cc = (cb * ncb + c) * 32 + 8 * (v >> 2) + 4 * g + (v & 3)
+                    if cc < Cout:
+                        part[split, cc, t, ci[ci_ok]] = lanes[g, ci_ok, v]
+                        hits[split, cc, t, ci[ci_ok]] += 1
+            if wv == 0 and gb == 0:
+                for c in range(ncb):
+                    ok = co[c] < Cout
+                    dbpart[split, co[c][ok]] = (dbs[c, 0] + dbs[c, 1])[ok]
+    assert seen == set(range(total))
+    assert (hits == 1).all() and not np.isnan(dbpart).any()
+    dw = part.sum(axis=0).reshape(Cout, 3, 3, 3, Cin).transpose(0, 4, 1, 2, 3)
+    return dw, dbpart.sum(axis=0)
+
+
+@pytest.mark.parametrize("sw", [1, 2])
+@pytest.mark.parametrize("cin,cout", [(8, 16), (40, 72)])
+@pytest.mark.parametrize("nsplit", [1, 5])
+def test_direct_dw_matches_conv3d_weight_grad(sw, cin, cout, nsplit):
+    rng = np.random.default_rng(3 * sw + cin + cout + nsplit)
+    stride, pad = (2, 1, sw), (1, 0, 1)
+    x_shape = (2, cin, 5, 3, 32)
+    wt_shape = (cout, cin, 3, 3, 3)
+    y_shape = (2, cout) + tuple((v + 2 * p - 3) // s + 1 for v, p, s in zip(x_shape[2:], pad, stride))
+    assert y_shape[4] % 16 == 0
+    x = rng.standard_normal(x_shape)
+    dy = rng.standard_normal(y_shape)
+    ref = torch.nn.grad.conv3d_weight(torch.from_numpy(x), wt_shape, torch.from_numpy(dy), stride, pad).numpy()
+    dw, db = replay_dw(x, dy, stride, pad, nsplit)
+    np.testing.assert_allclose(dw, ref, rtol=1e-12, atol=1e-10)
+    np.testing.assert_allclose(db, dy.sum(axis=(0, 2, 3, 4)), rtol=1e-12, atol=1e-10)
