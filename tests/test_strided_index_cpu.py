@@ -1,7 +1,8 @@
 """Index math of the strided kernels that stage source rows through LDS
 (csrc/r3c_strided.hip: strided_fwd_rs_kernel with an NDHWC source or an
-NCDHW one read in place, strided_dx_rs_kernel) and of the direct weight
-gradient (strided_dw_kernel), replayed on the CPU with numpy and checked
+NCDHW one read in place, strided_dx_rs_kernel), of the direct weight
+gradient (strided_dw_kernel) and of the dY scatter of the other dW path
+(dilate_kernel), replayed on the CPU with numpy and checked
 against PyTorch's float64 convolution and its gradients, with every LDS slot
 and every source element the replay touches asserted inside its buffer.
 
@@ -406,3 +407,60 @@ def test_direct_dw_matches_conv3d_weight_grad(sw, cin, cout, nsplit):
     dw, db = replay_dw(x, dy, stride, pad, nsplit)
     np.testing.assert_allclose(dw, ref, rtol=1e-12, atol=1e-10)
     np.testing.assert_allclose(db, dy.sum(axis=(0, 2, 3, 4)), rtol=1e-12, atol=1e-10)
+
+
+def replay_dilate(dy_flat, ys, N, C, D1, H1, W1, W1p, sd, sh, sw):
+    """dilate_kernel: thread gi writes elements w0 .. w0 + 7 (one 16-byte
+    store) of row (n, c, d1, h1) of the stride-1 grid, pitch W1p; element w1 is
+    dY at (d1 / sd, h1 / sh, w1 / sw) when all three divide, else zero."""
+    rows = N * C * D1 * H1
+    gpr = W1p >> 3
+    gi = np.arange(rows * gpr)
+    row, w0 = gi // gpr, (gi % gpr) * 8
+    h1 = row % H1
+    d1 = (row // H1) % D1
+    nc = row // H1 // D1
+    c, n = nc % C, nc // C
+    assert (w0 + 8 <= W1p).all() and W1p % 8 == 0
+    dst = np.full(rows * W1p, np.nan)
+    for e in range(8):
+        w1 = w0 + e
+        take = (w1 < W1) & (w1 % sw == 0) & (d1 % sd == 0) & (h1 % sh == 0)
+        off = n * ys[0] + c * ys[1] + (d1 // sd) * ys[2] + (h1 // sh) * ys[3] + (w1 // sw) * ys[4]
+        assert (off[take] >= 0).all() and (off[take] < dy_flat.size).all()
+        val = np.zeros(gi.size)
+        val[take] = dy_flat[off[take]]
+        dst[row * W1p + w1] = val
+    assert not np.isnan(dst).any()
+    return dst.reshape(N, C, D1, H1, W1p)
+
+
+@pytest.mark.parametrize("layout", ["ncdhw", "ndhwc"])
+@pytest.mark.parametrize("k,stride,pad", [(3, (2, 2, 2), (1, 1, 1)), (3, (2, 1, 3), (0, 1, 2)), (1, (2, 2, 2), (0, 0, 0)),
+                                          (3, (3, 2, 4), (2, 0, 1))])
+def test_dilated_dy_gives_the_strided_weight_grad(layout, k, stride, pad):
+    """The scatter dW path: dW of the strided convolution equals dW of the
+    stride-1 convolution (same input, padding, kernel) over dY scattered by
+    dilate_kernel into the stride-1 output grid (rows padded to 8)."""
+    rng = np.random.default_rng(sum(stride) * 10 + k + sum(pad))
+    N, ci, co = 2, 5, 16
+    x_shape = (N, ci, 7, 6, 13)
+    y_shape = (N, co) + tuple((v + 2 * p - k) // s + 1 for v, p, s in zip(x_shape[2:], pad, stride))
+    x = rng.standard_normal(x_shape)
+    dy = rng.standard_normal(y_shape)
+    if layout == "ndhwc":
+        store = dy.transpose(0, 2, 3, 4, 1).copy()
+        _, OD, OH, OW, _ = store.shape
+        ys = (OD * OH * OW * co, 1, OH * OW * co, OW * co, co)
+    else:
+        store = dy
+        ys = tuple(s // 8 for s in dy.strides)
+    D1, H1, W1 = (v + 2 * p - k + 1 for v, p in zip(x_shape[2:], pad))
+    W1p = (W1 + 7) // 8 * 8
+    dy1 = replay_dilate(store.reshape(-1), ys, N, co, D1, H1, W1, W1p, *stride)[..., :W1]
+    wt_shape = (co, ci, k, k, k)
+    ref = torch.nn.grad.conv3d_weight(torch.from_numpy(x), wt_shape, torch.from_numpy(dy), stride, pad).numpy()
+    got = torch.nn.grad.conv3d_weight(torch.from_numpy(x), wt_shape, torch.from_numpy(np.ascontiguousarray(dy1)), 1,
+                                      pad).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-10)
+    np.testing.assert_allclose(dy1.sum(axis=(0, 2, 3, 4)), dy.sum(axis=(0, 2, 3, 4)), rtol=1e-12, atol=1e-10)
