@@ -10,7 +10,10 @@ Per wave tile the replay follows the kernel step by step: the per-lane chunk
 table (position, 8-channel group) of a row segment, the zero-filled K-padding
 slots, the LDS slot of each chunk (pitch 2 NC + 1 slots per position), the
 segment position each (block, lane, tap) fragment read uses, and the taps of
-one residue class of w for dX (tap_range).  A plausible slip -- a wrong
+one residue class of w for dX (tap_range); the weight operand is the
+replayed strided_pack_kernel output, read at the kernels' own fragment
+addresses (the forward through the workgroup-shared stage copy s_w, dX from
+global memory).  A plausible slip -- a wrong
 segment origin, tap order, residue class or pitch -- changes the result or
 trips a bounds assertion.  For dW the replay also follows the x window's
 dword picks (v_alignbit / v_perm at 16-bit granularity), the K-block walk of
@@ -79,6 +82,39 @@ def run_segment_tile_cf(lds, wslots, src, n, row, iw0, segp, nc, cs, sw_len):
                 lds[slot] = block[:, p] if loaded else 0.0
 
 
+def replay_pack(wt, dx):
+    """strided_pack_kernel: fragment v = ((c16 taps + t) nbt + nb) 64 + lane
+    holds, for lane (li, g), K channels 16 c16 + 8 g + e (e = 0..7) of column
+    32 nb + li at tap t, zero past either channel count.  Forward: K = Cin,
+    column = Cout; dX: K = Cout, column = Cin (no tap flip).  One column tile
+    (the row-segment kernels take at most two 32-column blocks): nbt = the
+    32-column blocks."""
+    cout, cin, taps = wt.shape[0], wt.shape[1], wt[0, 0].size
+    kc, ncol = (cout, cin) if dx else (cin, cout)
+    nc16, nbt = -(-kc // 16), -(-ncol // 32)
+    wflat = wt.reshape(-1)
+    v = np.arange(nc16 * taps * nbt * 64)
+    lane, rest = v & 63, v >> 6
+    nb, rest = rest % nbt, rest // nbt
+    t, c16 = rest % taps, rest // taps
+    col, g = nb * 32 + (lane & 31), lane >> 5
+    out = np.zeros((v.size, 8))
+    for e in range(8):
+        kch = c16 * 16 + 8 * g + e
+        ok = (col < ncol) & (kch < kc)
+        co, ci = (kch, col) if dx else (col, kch)
+        idx = (co * cin + ci) * taps + t
+        assert (idx[ok] < wflat.size).all()
+        out[ok, e] = wflat[idx[ok]]
+    return out, nbt
+
+
+def _weight_matrix(lanes):
+    """The K x 32 operand of one 32x32x16 MFMA whose A fragment is the 64
+    lanes' weight vectors: lane (li, g) element e is row 8 g + e, column li."""
+    return np.concatenate([lanes[:32].T, lanes[32:].T], axis=0)
+
+
 def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
     """strided_fwd_rs_kernel on float64 x, NDHWC [n, D, H, W, Cs] (CF 0) or
     NCDHW [n, Cs, D, H, W] read in place (CF = Cs / 8); weight OIDHW."""
@@ -96,9 +132,9 @@ def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
     p_epi = 32 * ((co + 31) // 32) + 8
     wslots = max(segp * pps, 4 * p_epi)
     nwb = -(-OW // (32 * mb))
-    # packed weights: fragment (c16, tap) lane (li = co, g) -> W[co][16 c16 + 8 g + e][tap]
-    wk = np.zeros((nc * 16, 27, co))
-    wk[:cs] = wt.reshape(co, cs, 27).transpose(1, 2, 0)
+    pk, nbt = replay_pack(wt, dx=False)
+    nbw = nbt
+    wfr = 3 * nc * nbw * 64  # weight fragments of one (kd, kh) stage, shared by the workgroup
     y = np.zeros((n_, OD, OH, OW, co))
     for n, od, oh, wb in itertools.product(range(n_), range(OD), range(OH), range(nwb)):
         ow0 = wb * mb * 32
@@ -107,9 +143,16 @@ def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
         for pos in range(segp):  # K-padding groups stay zero
             for cg in range(cs // 8, 2 * nc):
                 lds[pos * pps + cg] = 0.0
-        acc = np.zeros((mb, 32, co))
+        acc = np.zeros((mb, 32, 32 * nbw))
         for st in range(9):
             kd, kh = divmod(st, 3)
+            s_w = np.zeros((wfr, 8))  # wissue(st) -> s_w, fragment f = ((kw NC + c) NB + nb) 64 + lane
+            for f in range(wfr):
+                ln, rest = f & 63, f >> 6
+                nb, c, kw = rest % nbw, (rest // nbw) % nc, rest // (nbw * nc)
+                src = ((c * 27 + st * 3 + kw) * nbt + nb) * 64 + ln
+                assert src < len(pk)
+                s_w[f] = pk[src]
             idd, ih = od * sd - pd + kd, oh * sh - ph + kh
             row = (idd, ih) if (0 <= idd < D and 0 <= ih < H) else None
             if channels_first:
@@ -123,12 +166,14 @@ def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
                     frag = np.concatenate([lds[((m * 32 + li) * sw + kw) * pps + 2 * c + g] for g in (0, 1)], axis=1)
                     slots = ((m * 32 + li) * sw + kw) * pps + 2 * c + 1
                     assert slots.max() < wslots
-                    acc[m] += frag @ wk[16 * c:16 * c + 16, t, :]
+                    for nb in range(nbw):
+                        f0 = ((kw * nc + c) * nbw + nb) * 64
+                        acc[m, :, 32 * nb:32 * nb + 32] += frag @ _weight_matrix(s_w[f0:f0 + 64])
         for m in range(mb):
             for li in range(32):
                 ow = ow0 + 32 * m + li
                 if ow < OW:
-                    y[n, od, oh, ow] = acc[m, li]
+                    y[n, od, oh, ow] = acc[m, li, :co]
     return y
 
 
@@ -144,9 +189,7 @@ def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
     p_epi = 32 * ((ci + 31) // 32) + 8
     wslots = max(segmax * pps, 4 * p_epi)
     nwb = -(-(-(-W // sw)) // (32 * mb))
-    # dX packing (strided_pack_kernel): K channel = Cout index, column = Cin index, tap t as is
-    wk = np.zeros((nc * 16, 27, ci))
-    wk[:cs] = wt.reshape(cs, ci, 27).transpose(0, 2, 1)
+    pk, nbt = replay_pack(wt, dx=True)
     dx = np.zeros((n_, D, H, W, ci))
     for n, rd, rh, res, wb in itertools.product(range(n_), range(D), range(H), range(sw), range(nwb)):
         td = tap_range(True, rd, pd, sd)
@@ -157,7 +200,7 @@ def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
         s0 = j0 + tw[3] - (tw[2] - 1 if tw[2] > 0 else 0)
         assert seg <= segmax
         lds = np.zeros((wslots, 8))
-        acc = np.zeros((mb, 32, ci))
+        acc = np.zeros((mb, 32, 32 * nbt))
         for md, mh in itertools.product(range(td[2]), range(th[2])):
             cd, ch = td[3] + md * td[4], th[3] + mh * th[4]
             kd, kh = td[0] + md * td[1], th[0] + mh * th[1]
@@ -172,12 +215,15 @@ def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
                     pos = m * 32 + li + pb
                     assert pos.max() < seg
                     frag = np.concatenate([lds[pos * pps + 2 * c + g] for g in (0, 1)], axis=1)
-                    acc[m] += frag @ wk[16 * c:16 * c + 16, t, :]
+                    for nb in range(nbt):  # wpk[((c taps + t) nbt + nb) 64 + lane], column tile 0
+                        f0 = ((c * 27 + t) * nbt + nb) * 64
+                        assert f0 + 64 <= len(pk)
+                        acc[m, :, 32 * nb:32 * nb + 32] += frag @ _weight_matrix(pk[f0:f0 + 64])
         for m in range(mb):
             for li in range(32):
                 w = res + sw * (j0 + 32 * m + li)
                 if w < W:
-                    dx[n, rd, rh, w] = acc[m, li]
+                    dx[n, rd, rh, w] = acc[m, li, :ci]
     return dx
 
 
@@ -185,11 +231,12 @@ def replay_dx(dy, wt, x_shape, stride, pad, mb, sw):
 @pytest.mark.parametrize("mb", [1, 2])
 @pytest.mark.parametrize("sw", [1, 2])
 @pytest.mark.parametrize("cs", [8, 24, 32])
-def test_fwd_row_segments_match_conv3d(mb, sw, cs, layout):
-    rng = np.random.default_rng(7 * mb + sw + cs)
+@pytest.mark.parametrize("co", [5, 40])
+def test_fwd_row_segments_match_conv3d(mb, sw, cs, layout, co):
+    rng = np.random.default_rng(7 * mb + sw + cs + co)
     stride, pad = (2, 1, sw), (1, 0, 1)
     x = rng.standard_normal((1, cs, 4, 4, 72))  # W % 8 == 0 (in-place NCDHW reads whole 8-position runs)
-    wt = rng.standard_normal((5, cs, 3, 3, 3))
+    wt = rng.standard_normal((co, cs, 3, 3, 3))
     ref = F.conv3d(torch.from_numpy(x), torch.from_numpy(wt), None, stride, pad).numpy()
     if layout == "ncdhw":
         y = replay_fwd(x, wt, stride, pad, mb, sw, channels_first=True)
@@ -201,10 +248,10 @@ def test_fwd_row_segments_match_conv3d(mb, sw, cs, layout):
 @pytest.mark.parametrize("mb", [1, 2])
 @pytest.mark.parametrize("sw", [1, 2])
 @pytest.mark.parametrize("cs", [8, 40, 64])
-def test_dx_row_segments_match_conv3d_input_grad(mb, sw, cs):
-    rng = np.random.default_rng(11 * mb + sw + cs)
+@pytest.mark.parametrize("ci", [6, 40])
+def test_dx_row_segments_match_conv3d_input_grad(mb, sw, cs, ci):
+    rng = np.random.default_rng(11 * mb + sw + cs + ci)
     stride, pad = (2, 1, sw), (1, 1, 1)
-    ci = 6
     x_shape = (1, ci, 5, 3, 67)
     wt = rng.standard_normal((cs, ci, 3, 3, 3))
     y_shape = (1, cs) + tuple((v + 2 * p - 3) // s + 1 for v, p, s in zip(x_shape[2:], pad, stride))
