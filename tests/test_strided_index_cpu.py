@@ -13,7 +13,10 @@ segment position each (block, lane, tap) fragment read uses, and the taps of
 one residue class of w for dX (tap_range); the weight operand is the
 replayed strided_pack_kernel output, read at the kernels' own fragment
 addresses (the forward through the workgroup-shared stage copy s_w, dX from
-global memory).  A plausible slip -- a wrong
+global memory); with Cout % 8 == 0 the forward's results leave through the
+dtile epilogue (accumulator lanes -> the wave's LDS block at pitch
+32 NB + 8 -> 16-byte rows of the NDHWC destination), each element read
+after it was written.  A plausible slip -- a wrong
 segment origin, tap order, residue class or pitch -- changes the result or
 trips a bounds assertion.  For dW the replay also follows the x window's
 dword picks (v_alignbit / v_perm at 16-bit granularity), the K-block walk of
@@ -115,6 +118,15 @@ def _weight_matrix(lanes):
     return np.concatenate([lanes[:32].T, lanes[32:].T], axis=0)
 
 
+def _mfma32_lanes(c):
+    """Accumulator registers of v_mfma_f32_32x32x16 for a 32 x 32 result C:
+    lane (li, g) register v holds C[8 (v // 4) + 4 g + v % 4][li]."""
+    out = np.zeros((2, 32, 16) + c.shape[2:])
+    for g, v in itertools.product(range(2), range(16)):
+        out[g, :, v] = c[8 * (v // 4) + 4 * g + v % 4]
+    return out
+
+
 def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
     """strided_fwd_rs_kernel on float64 x, NDHWC [n, D, H, W, Cs] (CF 0) or
     NCDHW [n, Cs, D, H, W] read in place (CF = Cs / 8); weight OIDHW."""
@@ -169,11 +181,32 @@ def replay_fwd(x, wt, stride, pad, mb, sw, channels_first=False):
                     for nb in range(nbw):
                         f0 = ((kw * nc + c) * nbw + nb) * 64
                         acc[m, :, 32 * nb:32 * nb + 32] += frag @ _weight_matrix(s_w[f0:f0 + 64])
-        for m in range(mb):
-            for li in range(32):
-                ow = ow0 + 32 * m + li
-                if ow < OW:
-                    y[n, od, oh, ow] = acc[m, li, :co]
+        if co % 8 == 0:  # dtile epilogue (dense NDHWC destination, Cout % 8 == 0)
+            pitch = 32 * nbw + 8
+            for m in range(mb):
+                w0 = ow0 + 32 * m
+                if w0 >= OW:
+                    break
+                tb = np.full(wslots * 8, np.nan)  # the wave's LDS block as halves
+                for nb in range(nbw):
+                    lanes = _mfma32_lanes(acc[m, :, 32 * nb:32 * nb + 32].T)  # rows = channels, columns = positions
+                    for g, q in itertools.product(range(2), range(4)):
+                        c0 = nb * 32 + 8 * q + 4 * g
+                        for li in range(32):
+                            assert (li * pitch + c0) % 4 == 0 and li * pitch + c0 + 4 <= tb.size
+                            tb[li * pitch + c0:li * pitch + c0 + 4] = lanes[g, li, 4 * q:4 * q + 4]
+                npos, cpp = min(32, OW - w0), co // 8
+                for k in range(npos * cpp):
+                    pos, c8 = divmod(k, cpp)
+                    src = pos * pitch + 8 * c8
+                    assert src % 8 == 0 and src + 8 <= tb.size and not np.isnan(tb[src:src + 8]).any()
+                    y[n, od, oh, w0 + pos, 8 * c8:8 * c8 + 8] = tb[src:src + 8]
+        else:
+            for m in range(mb):
+                for li in range(32):
+                    ow = ow0 + 32 * m + li
+                    if ow < OW:
+                        y[n, od, oh, ow] = acc[m, li, :co]
     return y
 
 
@@ -278,15 +311,6 @@ def _perm(hi, lo, sel):
         assert b0 % 2 == 0 and b1 == b0 + 1 and b0 < 8
         out.append(halves[b0 // 2])
     return tuple(out)
-
-
-def _mfma32_lanes(c):
-    """Accumulator registers of v_mfma_f32_32x32x16 for a 32 x 32 result C:
-    lane (li, g) register v holds C[8 (v // 4) + 4 g + v % 4][li]."""
-    out = np.zeros((2, 32, 16) + c.shape[2:])
-    for g, v in itertools.product(range(2), range(16)):
-        out[g, :, v] = c[8 * (v // 4) + 4 * g + v % 4]
-    return out
 
 
 def replay_dw(x, dy, stride, pad, nsplit):
