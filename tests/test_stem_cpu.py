@@ -1,0 +1,170 @@
+"""Index math of the one-input-channel k=3 forward (csrc/r3c_stem.hip:
+stem_fwd_kernel) replayed on the CPU in float64 and checked against
+PyTorch's conv3d.
+
+Per job (n, od, 4 output rows from oh0) the replay follows the kernel: the
+staging items (input row of the 3 x 6 staged rows, 16-byte group q; group 0
+and groups past the row are zeros, as are rows outside the volume) into the
+LDS tile [row][P] with input element w at 8 + w, P from the host planner
+(csrc/r3c_capi.hip stem_args); the weight operand (lane (co, g) holds taps
+16 m + 8 g .. +7, zero past tap 26); the tap-operand gather at
+wave row + 8 - pw + position + tap offset (kd * 6 + kh) * P + kw, with taps
+past 26 masked; the MFMA accumulator lane layout; and either the per-wave
+output block [channel][72] written 32 positions at a time and stored as
+8-position runs (positions contiguous, OW % 8 == 0) or the per-lane stores.
+Every LDS read, including those of lanes past OW, is asserted inside the
+staged tile, every output element is written exactly once.
+"""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+ROWS = 4            # output rows per job, one wave each
+XROWS = 3 * (ROWS + 2)
+LOADS, THREADS = 5, 256
+TP = 72             # output block pitch (positions per channel row)
+
+
+def _mfma32_lanes(c):
+    """v_mfma_f32_32x32x16 accumulators: lane (li, g) register v holds C[8 (v // 4) + 4 g + v % 4][li]."""
+    out = np.zeros((2, 32, 16))
+    for g, v in itertools.product(range(2), range(16)):
+        out[g, :, v] = c[8 * (v // 4) + 4 * g + v % 4]
+    return out
+
+
+def stem_pitch(W, OW):
+    return (max(W, -(-OW // 32) * 32) + 18 + 7) // 8 * 8
+
+
+def replay_stem_fwd(x, w, b, pad, yvec8):
+    """x [N, D, H, W] (one channel), w [Cout, 27], b [Cout]: y [N, Cout, OD, OH, OW]."""
+    N, D, H, W = x.shape
+    cout = w.shape[0]
+    pd, ph, pw = pad
+    OD, OH, OW = D + 2 * pd - 2, H + 2 * ph - 2, W + 2 * pw - 2
+    P = stem_pitch(W, OW)
+    gpr = P >> 3
+    total = XROWS * gpr
+    assert total <= LOADS * THREADS
+    nb_n = 1 if cout <= 32 else 2
+    nrb = -(-OH // ROWS)
+    y = np.full((N, cout, OD, OH, OW), np.nan)
+    hits = np.zeros(y.shape, dtype=np.int64)
+    # weight operand: wa[nb][m] lane (li, g) element e = w[32 nb + li][16 m + 8 g + e]
+    wa = np.zeros((nb_n, 2, 64, 8))
+    for nb, m, g, li, e in itertools.product(range(nb_n), range(2), range(2), range(32), range(8)):
+        co, t = nb * 32 + li, 16 * m + 8 * g + e
+        if co < cout and t < 27:
+            wa[nb, m, 32 * g + li, e] = w[co, t]
+    toff = np.zeros((2, 2, 8), dtype=np.int64)  # [g][m][e]
+    for g, m, e in itertools.product(range(2), range(2), range(8)):
+        t = 16 * m + 8 * g + e
+        kd, kh, kw = t // 9, (t // 3) % 3, t % 3
+        toff[g, m, e] = (kd * (ROWS + 2) + kh) * P + kw if t < 27 else 0
+    for job in range(N * OD * nrb):
+        rb, t = job % nrb, job // nrb
+        od, n = t % OD, t // OD
+        oh0 = rb * ROWS
+        xs = np.zeros(XROWS * P)
+        for i in range(total):
+            row, q = divmod(i, gpr)
+            kd, rr = divmod(row, ROWS + 2)
+            idd, ih = od - pd + kd, oh0 - ph + rr
+            if 1 <= q <= W // 8 and 0 <= idd < D and 0 <= ih < H:
+                xs[i * 8:i * 8 + 8] = x[n, idd, ih, (q - 1) * 8:q * 8]
+        for wv in range(ROWS):
+            oh = oh0 + wv
+            if oh >= OH:
+                continue
+            rowb = wv * P + 8 - pw
+            tb = np.full((32 * nb_n, TP), np.nan)
+            step = 64 if yvec8 else 32
+            for w0 in range(0, OW, step):
+                for h in range(2):
+                    wt = w0 + 32 * h
+                    if h == 1 and (not yvec8 or wt >= OW):
+                        break
+                    bx = np.zeros((2, 64, 8))  # [m][lane][e]
+                    for g, li in itertools.product(range(2), range(32)):
+                        idx = rowb + wt + li + toff[g]
+                        assert idx.min() >= 0 and idx.max() < xs.size
+                        bx[:, 32 * g + li] = xs[idx]
+                        if g:  # taps 27 .. 31 of the second product
+                            bx[1, 32 * g + li, 3:] = 0.0
+                    for nb in range(nb_n):
+                        acc = np.zeros((32, 32))  # [co][position]
+                        for m in range(2):
+                            amat = np.concatenate([wa[nb, m, :32], wa[nb, m, 32:]], axis=1)   # [co][16 taps]
+                            bmat = np.concatenate([bx[m, :32].T, bx[m, 32:].T], axis=0)      # [16 taps][position]
+                            acc += amat @ bmat
+                        lanes = _mfma32_lanes(acc)
+                        for g, li, v in itertools.product(range(2), range(32), range(16)):
+                            co = nb * 32 + 8 * (v >> 2) + 4 * g + (v & 3)
+                            val = lanes[g, li, v] + (b[co] if co < cout else 0.0)
+                            if yvec8:
+                                tb[co, 32 * h + li] = val
+                            elif wt + li < OW and co < cout:
+                                y[n, co, od, oh, wt + li] = val
+                                hits[n, co, od, oh, wt + li] += 1
+                if yvec8:
+                    for it in range(cout * 8):
+                        co, sg = it >> 3, it & 7
+                        p0 = w0 + 8 * sg
+                        if p0 < OW:
+                            assert p0 + 8 <= OW and 8 * sg + 8 <= TP
+                            seg = tb[co, 8 * sg:8 * sg + 8]
+                            assert not np.isnan(seg).any()
+                            y[n, co, od, oh, p0:p0 + 8] = seg
+                            hits[n, co, od, oh, p0:p0 + 8] += 1
+    assert (hits == 1).all()
+    return y
+
+
+@pytest.mark.parametrize("with_inf", [False, True])
+@pytest.mark.parametrize("yvec8", [True, False])
+@pytest.mark.parametrize("cout,dhw,pad", [
+    (8, (3, 5, 16), (1, 1, 1)),
+    (40, (3, 7, 40), (0, 2, 1)),   # two channel blocks, OH 9: a partial job of rows
+    (24, (4, 4, 64), (2, 1, 2)),   # OW 66 (per-lane stores) / rows longer than one 64-position pair
+])
+def test_stem_forward_replay_matches_conv3d(yvec8, cout, dhw, pad, with_inf):
+    """with_inf: one infinite input element; the outputs that read it are
+    +-inf, not NaN, only if the taps past 26 (which read tap 0's element)
+    are masked rather than multiplied by zero weights."""
+    D, H, W = dhw
+    OW = W + 2 * pad[2] - 2
+    if yvec8 and OW % 8:
+        pytest.skip("8-position runs need OW % 8 == 0 (the host's yvec8 condition)")
+    rng = np.random.default_rng(cout + sum(dhw) + sum(pad) + yvec8)
+    N = 2
+    x = rng.standard_normal((N, D, H, W))
+    if with_inf:
+        x[1, 1, 2, 5] = np.inf
+    w = rng.standard_normal((cout, 27))
+    b = rng.standard_normal(cout)
+    with np.errstate(invalid="ignore"):
+        y = replay_stem_fwd(x, w, b, pad, yvec8)
+    ref = F.conv3d(torch.from_numpy(x[:, None]), torch.from_numpy(w.reshape(cout, 1, 3, 3, 3)),
+                   torch.from_numpy(b), padding=pad).numpy()
+    assert not np.isnan(ref).any() and (np.isinf(ref).sum() > 0) == with_inf
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-10)
+
+
+def test_stem_pitch_covers_the_widest_rows():
+    """Staging fits its 5 loads per thread at the widest admitted row, and
+    every tap read of the last 32-position tile stays inside its row."""
+    for W in range(8, 513, 8):
+        for pw in range(3):
+            OW = W + 2 * pw - 2
+            if OW > 512:
+                continue
+            P = stem_pitch(W, OW)
+            assert XROWS * (P >> 3) <= LOADS * THREADS
+            last = -(-OW // 32) * 32 - 1
+            assert 8 - pw + last + 2 < P and 8 + W <= P
