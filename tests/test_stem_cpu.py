@@ -1,5 +1,5 @@
-"""Index math of the one-input-channel k=3 forward (csrc/r3c_stem.hip:
-stem_fwd_kernel) replayed on the CPU in float64 and checked against
+"""Index math of the one-input-channel k=3 forward and weight gradient
+(csrc/r3c_stem.hip: stem_fwd_kernel, stem_dw_kernel) replayed on the CPU in float64 and checked against
 PyTorch's conv3d.
 
 Per job (n, od, 4 output rows from oh0) the replay follows the kernel: the
@@ -13,7 +13,10 @@ past 26 masked; the MFMA accumulator lane layout; and either the per-wave
 output block [channel][72] written 32 positions at a time and stored as
 8-position runs (positions contiguous, OW % 8 == 0) or the per-lane stores.
 Every LDS read, including those of lanes past OW, is asserted inside the
-staged tile, every output element is written exactly once.
+staged tile, every output element is written exactly once.  For dW: jobs
+dealt to workgroups with a grid stride, the 12-element window and kw shift of
+each tap lane, the all-ones tap column 27 that yields db, the wave-order sum
+and the partial slots (each written once), against torch's conv3d_weight.
 """
 from __future__ import annotations
 
@@ -168,3 +171,104 @@ def test_stem_pitch_covers_the_widest_rows():
             assert XROWS * (P >> 3) <= LOADS * THREADS
             last = -(-OW // 32) * 32 - 1
             assert 8 - pw + last + 2 < P and 8 + W <= P
+
+
+def replay_stem_dw(x, dy, pad, nsplit_max=1024):
+    """stem_dw_kernel + the fixed-order reduce: x [N, D, H, W], dy [N, Cout,
+    OD, OH, OW] (OW % 16 == 0) -> (dw [Cout, 27], db [Cout]).  Lane (t = li,
+    g) of the tap operand takes 8 positions from the 12-element LDS window
+    [base - 2, base + 10) around its row's element, offset o = kw - pw + 2
+    (dword o // 2, plus one element when o is odd: v_alignbit); tap column 27
+    is all ones (db), 28-31 zero."""
+    N, D, H, W = x.shape
+    cout, OD, OH, OW = dy.shape[1:]
+    pd, ph, pw = pad
+    assert OW % 16 == 0 and W % 8 == 0
+    P = stem_pitch(W, OW)
+    gpr = P >> 3
+    nb_n = 1 if cout <= 32 else 2
+    nrb = -(-OH // ROWS)
+    njobs = N * OD * nrb
+    nsplit = min(njobs, nsplit_max)
+    part = np.full((nsplit, cout, 27), np.nan)
+    dbpart = np.full((nsplit, cout), np.nan)
+    hits = np.zeros(part.shape, dtype=np.int64)
+    for blk in range(nsplit):
+        acc = np.zeros((ROWS, nb_n, 32, 32))  # [wave][nb][co][tap]
+        for job in range(blk, njobs, nsplit):
+            rb, t = job % nrb, job // nrb
+            od, n = t % OD, t // OD
+            oh0 = rb * ROWS
+            xs = np.zeros(XROWS * P)
+            for i in range(XROWS * gpr):
+                row, q = divmod(i, gpr)
+                kd, rr = divmod(row, ROWS + 2)
+                idd, ih = od - pd + kd, oh0 - ph + rr
+                if 1 <= q <= W // 8 and 0 <= idd < D and 0 <= ih < H:
+                    xs[i * 8:i * 8 + 8] = x[n, idd, ih, (q - 1) * 8:q * 8]
+            for wv in range(ROWS):
+                oh = oh0 + wv
+                if oh >= OH:
+                    continue
+                for w0 in range(0, OW, 128):
+                    for kb in range(8):
+                        p0 = w0 + 16 * kb
+                        if p0 >= OW:
+                            break
+                        bmat = np.zeros((16, 32))  # [position 8 g + e][tap]
+                        for g, tap in itertools.product(range(2), range(32)):
+                            kd, kh, kw = tap // 9, (tap // 3) % 3, tap % 3
+                            o = (kw if tap < 27 else 1) - pw + 2
+                            roff = ((kd * (ROWS + 2) + kh if tap < 27 else 0) + wv) * P + 8 + 8 * g
+                            base = roff + p0
+                            assert base - 2 >= 0 and base + 10 <= xs.size and base % 8 == 0
+                            win = xs[base - 2:base + 10]
+                            vals = win[o:o + 8]
+                            if tap == 27:
+                                vals = np.ones(8)
+                            elif tap > 27:
+                                vals = np.zeros(8)
+                            bmat[8 * g:8 * g + 8, tap] = vals
+                        for nb in range(nb_n):
+                            amat = np.zeros((32, 16))  # [co][position]
+                            for li in range(32):
+                                co = nb * 32 + li
+                                if co < cout:
+                                    amat[li] = dy[n, co, od, oh, p0:p0 + 16]
+                            acc[wv, nb] += amat @ bmat
+        red = np.array([[_mfma32_lanes(acc[wv, nb]) for nb in range(nb_n)] for wv in range(ROWS)])
+        tot = ((red[0] + red[1]) + red[2]) + red[3]  # [nb][g][li][v]
+        for nb, g, li, v in itertools.product(range(nb_n), range(2), range(32), range(16)):
+            lane = 32 * g + li
+            co, tt = nb * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3), lane & 31
+            if co < cout:
+                if tt < 27:
+                    part[blk, co, tt] = tot[nb, g, li, v]
+                    hits[blk, co, tt] += 1
+                elif tt == 27:
+                    dbpart[blk, co] = tot[nb, g, li, v]
+    assert (hits == 1).all() and not np.isnan(dbpart).any()
+    return part.sum(axis=0), dbpart.sum(axis=0)
+
+
+@pytest.mark.parametrize("cout,dhw,pad,nsplit_max", [
+    (8, (3, 5, 16), (1, 1, 1), 1024),
+    (40, (3, 7, 32), (0, 2, 1), 2),    # two channel blocks, OH 9 (a partial job), 2 workgroups
+    (24, (4, 4, 144), (2, 1, 1), 3),   # OW 144: two 128-position segments
+])
+def test_stem_dw_replay_matches_conv3d_weight_grad(cout, dhw, pad, nsplit_max):
+    """W % 8 == 0 and OW % 16 == 0 leave w padding 1 as the only one the dW
+    kernel is given (csrc/r3c_capi.hip stem_ok), so the cases use it."""
+    D, H, W = dhw
+    OD, OH, OW = (v + 2 * p - 2 for v, p in zip(dhw, pad))
+    if OW % 16:
+        pytest.skip("the dW kernel needs OW % 16 == 0")
+    rng = np.random.default_rng(cout + W + nsplit_max)
+    N = 2
+    x = rng.standard_normal((N, D, H, W))
+    dy = rng.standard_normal((N, cout, OD, OH, OW))
+    dw, db = replay_stem_dw(x, dy, pad, nsplit_max)
+    ref = torch.nn.grad.conv3d_weight(torch.from_numpy(x[:, None]), (cout, 1, 3, 3, 3), torch.from_numpy(dy),
+                                      padding=pad).numpy().reshape(cout, 27)
+    np.testing.assert_allclose(dw, ref, rtol=1e-12, atol=1e-10)
+    np.testing.assert_allclose(db, dy.sum(axis=(0, 2, 3, 4)), rtol=1e-12, atol=1e-10)
